@@ -1,0 +1,341 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused QKV + gate-up-SiLU projections on one MI355X.
+
+A step is one pass of the hot path over a Qwen3 decoder stack: for each of
+``--layers`` (36) layers, the fused QKV projection then the fused gate-up-SiLU,
+each layer with its own weight set (N(0, 0.02) bf16), so the 4.72 GB working
+set of Qwen3-4B is far above the 256 MB Infinity Cache. Inputs x ~ N(0, 1)
+are resident in HBM before timing starts. The step's 72 launches are captured
+once in a HIP graph and replayed.
+
+Headline (BASELINE.json metric): HBM GB/s at M=1 on Qwen3-4B shapes =
+algorithmic bytes per layer pair (2K(N_qkv+2I) + 4MK + 2M(N_qkv+I)) x layers /
+step time. Also reported: TFLOP/s at M=2048 (prefill), the dominant kernel's
+roofline (per-launch HIP events on its stream), and the reference's unfused
+torch path timed on this host's CPU cores.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, GB/s
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "HBM GB/s (% peak) fused QKV+gate-up-SiLU Qwen3-4B M=1; TFLOPS at M=2048"
+
+# (K, n_q, n_k, I)
+SHAPES = {
+    "qwen3-0.6b": (1024, 2048, 1024, 3072),
+    "qwen3-4b": (2560, 4096, 1024, 9728),
+    "qwen3-8b": (4096, 4096, 1024, 12288),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def pair_bytes(M: int, K: int, n_qkv: int, inter: int) -> int:
+    """Algorithmic HBM bytes of one (QKV, gate-up) layer pair."""
+    return 2 * K * (n_qkv + 2 * inter) + 4 * M * K + 2 * M * (n_qkv + inter)
+
+
+def gate_up_bytes(M: int, K: int, inter: int) -> int:
+    return 2 * K * 2 * inter + 2 * M * K + 2 * M * inter
+
+
+def pair_flops(M: int, K: int, n_qkv: int, inter: int) -> int:
+    return 2 * M * K * (n_qkv + 2 * inter)
+
+
+class Stack:
+    """Per-layer weights and inputs for one shape, resident on the GPU."""
+
+    def __init__(self, torch, shape, layers: int, M: int, seed: int = 0):
+        K, n_q, n_k, inter = shape
+        self.K, self.n_q, self.n_k, self.I = K, n_q, n_k, inter
+        self.n_qkv = n_q + 2 * n_k
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        bf = torch.bfloat16
+
+        def w(rows):
+            return (torch.randn(rows, K, generator=g, device="cuda") * 0.02).to(bf)
+
+        self.wqkv = [w(self.n_qkv) for _ in range(layers)]
+        self.wg = [w(inter) for _ in range(layers)]
+        self.wu = [w(inter) for _ in range(layers)]
+        self.set_m(torch, M, g)
+
+    def set_m(self, torch, M: int, g=None):
+        self.M = M
+        self.x_attn = torch.randn(M, self.K, generator=g, device="cuda").to(torch.bfloat16)
+        self.x_ffn = torch.randn(M, self.K, generator=g, device="cuda").to(torch.bfloat16)
+
+
+def run_step(stack: Stack, kern) -> None:
+    for l in range(len(stack.wqkv)):
+        kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=stack.n_q, n_k=stack.n_k)
+        kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l])
+
+
+def capture(torch, fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(torch, graph, steps: int, warmup: int) -> float:
+    """Seconds per replay over `steps` replays (after `warmup`), bracketed by
+    synchronisations."""
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / 1e3 / steps
+
+
+def time_launches(torch, launches: list, reps: int) -> list[float]:
+    """Per-launch durations (s) from HIP event pairs recorded on the stream the
+    kernels are launched on (torch's current stream)."""
+    evs = []
+    for _ in range(reps):
+        for fn in launches:
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            evs.append((a, b))
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) / 1e3 for a, b in evs]
+
+
+def cpu_baseline(shape, M: int, sets: int, reps: int) -> dict:
+    """The reference's unfused torch path (oracle.torch_path) on the host CPU,
+    bf16, a bounded sample: `sets` distinct layer weight sets cycled."""
+    import torch
+
+    from oracle import torch_path as tp
+
+    K, n_q, n_k, inter = shape
+    aff = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", aff) or aff)
+    threads = max(1, min(aff, share))
+    torch.set_num_threads(threads)
+    g = torch.Generator()
+    g.manual_seed(1)
+    bf = torch.bfloat16
+    x1 = torch.randn(M, K, generator=g).to(bf)
+    x2 = torch.randn(M, K, generator=g).to(bf)
+    W = [((torch.randn(n_q + 2 * n_k, K, generator=g) * 0.02).to(bf),
+          (torch.randn(inter, K, generator=g) * 0.02).to(bf),
+          (torch.randn(inter, K, generator=g) * 0.02).to(bf)) for _ in range(sets)]
+    for wq, wg, wu in W[:2]:  # warmup
+        tp.torch_qkv(x1, wq, n_q, n_k)
+        tp.torch_gate_up_silu(x2, wg, wu)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for wq, wg, wu in W:
+            tp.torch_qkv(x1, wq, n_q, n_k)
+            tp.torch_gate_up_silu(x2, wg, wu)
+        times.append((time.perf_counter() - t0) / sets)
+    per_pair = statistics.median(times)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    gbs = pair_bytes(M, K, n_q + 2 * n_k, inter) / per_pair / 1e9
+    return {
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle/torch_path.py unfused bf16 torch path (F.linear+split, "
+                   f"F.silu(F.linear)*F.linear) on CPU, Qwen3-4B shapes M={M}, {sets} distinct "
+                   f"layer weight sets cycled, median of {reps} passes; "
+                   f"{per_pair * 1e3:.2f} ms per layer pair; cpu: {model}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--model", default="qwen3-4b", choices=sorted(SHAPES))
+    ap.add_argument("--prefill-m", type=int, default=2048)
+    ap.add_argument("--cpu-sets", type=int, default=8)
+    ap.add_argument("--cpu-reps", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only; the fused projections shard "
+              "by output columns with no collective inside the path (see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from llms_amd import kernels as kern
+    from llms_amd import ops
+
+    ops()  # load the HIP extension or fail loudly
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 2
+    dev_name = torch.cuda.get_device_name(0)
+    shape = SHAPES[args.model]
+    K, n_q, n_k, inter = shape
+    n_qkv = n_q + 2 * n_k
+    L = args.layers
+
+    # ---------------- decode, M = 1: the headline ----------------
+    log(f"device {dev_name}; allocating {L} layer weight sets of {args.model}")
+    stack = Stack(torch, shape, L, M=1)
+    torch.cuda.synchronize()
+    graph = capture(torch, lambda: run_step(stack, kern))
+    log("decode graph captured; timing")
+    sec = time_graph(torch, graph, args.steps, args.warmup)
+    bytes_step = L * pair_bytes(1, K, n_qkv, inter)
+    value = bytes_step / sec / 1e9
+    log(f"decode M=1: {sec * 1e6:.1f} us/step, {value:.1f} GB/s")
+
+    # eager (no graph) for reference
+    for _ in range(2):
+        run_step(stack, kern)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run_step(stack, kern)
+    torch.cuda.synchronize()
+    sec_eager = (time.perf_counter() - t0) / args.steps
+
+    # dominant kernel (gate-up, 76% of the bytes): per-launch HIP events
+    gu = [(lambda l=l: kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l]))
+          for l in range(L)]
+    qk = [(lambda l=l: kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k))
+          for l in range(L)]
+    time_launches(torch, gu, 1)
+    d_gu = statistics.mean(time_launches(torch, gu, max(2, args.steps // 4)))
+    d_qk = statistics.mean(time_launches(torch, qk, max(2, args.steps // 4)))
+    gu_gbs = gate_up_bytes(1, K, inter) / d_gu / 1e9
+    qk_gbs = (2 * K * n_qkv + 2 * K + 2 * n_qkv) / d_qk / 1e9
+    log(f"gate-up M=1: {d_gu * 1e6:.2f} us/launch {gu_gbs:.1f} GB/s; "
+        f"qkv M=1: {d_qk * 1e6:.2f} us/launch {qk_gbs:.1f} GB/s")
+    del graph
+
+    # ---------------- prefill ----------------
+    prefill = None
+    if not args.no_prefill:
+        Mp = args.prefill_m
+        stack.set_m(torch, Mp)
+        torch.cuda.synchronize()
+        graph = capture(torch, lambda: run_step(stack, kern))
+        psteps = max(3, args.steps // 4)
+        psec = time_graph(torch, graph, psteps, max(1, args.warmup // 2))
+        tflops = L * pair_flops(Mp, K, n_qkv, inter) / psec / 1e12
+        dp_gu = statistics.mean(time_launches(torch, gu, 2))
+        dp_qk = statistics.mean(time_launches(torch, qk, 2))
+        prefill = {
+            "M": Mp,
+            "tflops": round(tflops, 1),
+            "frac_of_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+            "us_per_layer_pair": round(psec / L * 1e6, 2),
+            "gate_up_us": round(dp_gu * 1e6, 2),
+            "gate_up_tflops": round(2 * Mp * K * 2 * inter / dp_gu / 1e12, 1),
+            "qkv_us": round(dp_qk * 1e6, 2),
+            "qkv_tflops": round(2 * Mp * K * n_qkv / dp_qk / 1e12, 1),
+        }
+        log(f"prefill M={Mp}: {prefill}")
+        del graph
+
+    del stack
+    torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline(shape, 1, args.cpu_sets, args.cpu_reps)
+        log(f"cpu: {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: x~N(0,1), W~N(0,0.02) bf16, random-init, fixed seeds",
+        "config": {
+            "workload": f"{args.model} fused QKV ({K}->{n_qkv}) + gate-up-SiLU "
+                        f"({K}->2x{inter}) per layer, M=1 decode, {L} distinct layer weight "
+                        f"sets cycled ({L * 2 * K * (n_qkv + 2 * inter) / 1e9:.2f} GB), "
+                        "one HIP graph per step",
+            "model_shapes": args.model,
+            "M": 1,
+            "layers": L,
+            "bytes_per_step": bytes_step,
+        },
+        "hbm_frac": round(value / PEAK_HBM_GBS, 4),
+        "eager_ms_per_step": round(sec_eager * 1e3, 4),
+        "decode_kernels": {
+            "gate_up_us": round(d_gu * 1e6, 3),
+            "qkv_us": round(d_qk * 1e6, 3),
+            "qkv_gbs": round(qk_gbs, 1),
+        },
+        "roofline": {
+            "kernel": "gate-up-SiLU bf16 M=1 (stream_kernel)",
+            "bound": "hbm",
+            "achieved": round(gu_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / PEAK_HBM_GBS, 4),
+            "traffic": None,
+        },
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+        "device": dev_name,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,123 @@
+/*
+ * llms_amd_fp.h — C ABI of the MI355X (gfx950) fused projection kernels.
+ *
+ * Two fused projections of a Qwen3 decoder layer, each as one contraction
+ * over a row-stacked weight:
+ *
+ *   QKV          y[M, n_q+2*n_k] = x[M,K] . [Wq;Wk;Wv]^T      (split done by the caller, as views)
+ *   gate-up-SiLU y[M, N]         = silu(x . Wg^T) * (x . Wu^T)
+ *
+ * plus per-output-channel symmetric int8 weight-only variants that
+ * dequantise w = bf16(float(q) * s[row]) in registers.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers. Element types: bf16 = raw 16-bit
+ *     bfloat16 (passed as void*), int8 weights, fp32 scales.
+ *   - Matrices are row-major with unit inner stride; ld* is the row
+ *     stride in ELEMENTS. Weights use the nn.Linear layout [N, K].
+ *   - stream is a hipStream_t (NULL = the legacy default stream). Every call
+ *     is asynchronous on that stream; nothing is allocated, freed or
+ *     synchronised; no global state is written; calls are reentrant.
+ *   - Return 0 (FP_OK) on success, a nonzero fp_status otherwise; argument
+ *     errors are detected before anything is launched.
+ *   - Results are deterministic: the same inputs give bit-identical outputs
+ *     on every call (fixed-order reductions, no atomics).
+ *
+ * Rounding contract (bf16 in, fp32 accumulate, bf16 out):
+ *   QKV:      y = bf16(sum_k x*w)
+ *   gate-up:  g = bf16(sum x*wg); u = bf16(sum x*wu);
+ *             s = bf16(g / (1 + exp(-g)));  y = bf16(s * u)
+ *   i.e. the rounding points of the unfused torch path
+ *   F.silu(F.linear(x, Wg)) * F.linear(x, Wu) in bfloat16.
+ *   int8:     w = bf16(float(q) * s[row]) then the bf16 contract above
+ *   (the "dequantise then matmul" path).
+ */
+#ifndef LLMS_AMD_FP_H
+#define LLMS_AMD_FP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum fp_status {
+  FP_OK = 0,
+  FP_ERR_NULL = 1,       /* a required pointer is NULL */
+  FP_ERR_SHAPE = 2,      /* M, N, K, n_q, n_k out of range or inconsistent */
+  FP_ERR_STRIDE = 3,     /* a row stride is smaller than the row length */
+  FP_ERR_LAUNCH = 4,     /* the HIP launch reported an error */
+  FP_ERR_DEVICE = 5      /* no usable gfx950 device for the current context */
+} fp_status;
+
+/* Human-readable text for an fp_status value (static storage). */
+const char* fp_status_string(int status);
+
+/* ABI version of this library: (major << 16) | minor. */
+int fp_abi_version(void);
+
+/*
+ * Fused QKV projection.
+ * Replaces _qkv_matmul_kernel + the launch in triton_fused_qkv
+ * (reference: src/kernels/fused_qkv.py:28-85, :131-145).
+ *   x  [M, K]            bf16, row stride ldx
+ *   w  [n_q+2*n_k, K]    bf16, row stride ldw  (row-stacked [Wq; Wk; Wv])
+ *   y  [M, n_q+2*n_k]    bf16, row stride ldy  (q | k | v column blocks)
+ * M >= 0 (M == 0 is a no-op), K >= 1, n_q >= 1, n_k >= 0.
+ */
+int fp_qkv_bf16(const void* x, int64_t ldx,
+                const void* w, int64_t ldw,
+                void* y, int64_t ldy,
+                int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+                void* stream);
+
+/*
+ * Fused gate-up-SiLU.
+ * Replaces _fused_gate_up_silu_kernel + the launch in
+ * triton_fused_gate_up_silu (reference: src/kernels/fused_ffn.py:20-95,
+ * :131-150). Wg and Wu stay two separate [N, K] buffers, as in the reference.
+ *   y [M, N] = silu(x Wg^T) * (x Wu^T)
+ */
+int fp_gate_up_silu_bf16(const void* x, int64_t ldx,
+                         const void* wg, int64_t ldwg,
+                         const void* wu, int64_t ldwu,
+                         void* y, int64_t ldy,
+                         int64_t M, int64_t N, int64_t K,
+                         void* stream);
+
+/*
+ * int8 weight-only QKV (no reference counterpart: the reference names
+ * weight quantisation only as future work, DESIGN.md:120).
+ *   q [n_q+2*n_k, K] int8 (row stride ldq), scale [n_q+2*n_k] fp32.
+ */
+int fp_qkv_w8(const void* x, int64_t ldx,
+              const int8_t* q, int64_t ldq, const float* scale,
+              void* y, int64_t ldy,
+              int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+              void* stream);
+
+/* int8 weight-only gate-up-SiLU (no reference counterpart, as above). */
+int fp_gate_up_silu_w8(const void* x, int64_t ldx,
+                       const int8_t* qg, int64_t ldqg, const float* sg,
+                       const int8_t* qu, int64_t ldqu, const float* su,
+                       void* y, int64_t ldy,
+                       int64_t M, int64_t N, int64_t K,
+                       void* stream);
+
+/*
+ * Per-output-channel symmetric int8 quantisation on the device (the packing
+ * step run once at swap time; no reference counterpart).
+ *   s[r] = max_k |w[r,k]| / 127   (fp32; rows that are all zero get s = 0)
+ *   q[r,k] = clamp(rne(w[r,k] / s[r]), -127, 127)   (0 where s == 0)
+ */
+int fp_quantize_w8_per_row(const void* w, int64_t ldw,
+                           int8_t* q, int64_t ldq, float* scale,
+                           int64_t N, int64_t K,
+                           void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* LLMS_AMD_FP_H */

@@ -1,0 +1,158 @@
+// fp_api.hip — the extern "C" entry points of include/llms_amd_fp.h:
+// argument validation (before any launch), regime dispatch and the
+// per-row int8 quantisation kernel.
+#include "llms_amd_fp.h"
+
+#include "fp_common.h"
+#include "fp_launch.h"
+
+namespace fp {
+
+namespace {
+
+// One workgroup per weight row: absmax reduction, then quantise the row.
+__global__ __launch_bounds__(256) void quantize_w8_kernel(const uint16_t* w, int64_t ldw,
+                                                          int8_t* q, int64_t ldq, float* scale,
+                                                          int64_t K) {
+  const int64_t r = blockIdx.x;
+  const uint16_t* wr = w + r * ldw;
+  float mx = 0.f;
+  for (int64_t k = threadIdx.x; k < K; k += blockDim.x) mx = fmaxf(mx, fabsf(bf16_bits_to_f32(wr[k])));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  __shared__ float part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+  const float s = mx / 127.0f;
+  if (threadIdx.x == 0) scale[r] = s;
+  int8_t* qr = q + r * ldq;
+  for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
+    float v = 0.f;
+    if (s > 0.f) v = fminf(fmaxf(rintf(bf16_bits_to_f32(wr[k]) / s), -127.f), 127.f);
+    qr[k] = (int8_t)(int)v;
+  }
+}
+
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// rc is the hipError_t of the launch (hipGetLastError right after it).
+int launch_status(int rc) {
+  if (rc == (int)hipSuccess) return FP_OK;
+  const hipError_t e = (hipError_t)rc;
+  if (e == hipErrorNoBinaryForGpu || e == hipErrorInvalidDeviceFunction) return FP_ERR_DEVICE;
+  return FP_ERR_LAUNCH;
+}
+
+template <bool GATEUP, bool W8>
+int run(const StreamArgs& a, bool aligned, hipStream_t s) {
+  if (a.M == 0) return FP_OK;
+  const int rc = (a.M <= kStreamMaxM) ? launch_stream<GATEUP, W8>(a, aligned, s)
+                                      : launch_tiled<GATEUP, W8>(a, aligned, s);
+  return launch_status(rc);
+}
+
+int check_common(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
+  if (M < 0 || N < 1 || K < 1) return FP_ERR_SHAPE;
+  // grid.x = ceil(N / 16) must fit a 32-bit grid dimension; M tiles likewise.
+  if (N > (int64_t)1 << 34 || M > (int64_t)1 << 34) return FP_ERR_SHAPE;
+  if (ldx < K || ldy < N) return FP_ERR_STRIDE;
+  return FP_OK;
+}
+
+}  // namespace
+}  // namespace fp
+
+using fp::StreamArgs;
+
+extern "C" {
+
+const char* fp_status_string(int status) {
+  switch (status) {
+    case FP_OK: return "ok";
+    case FP_ERR_NULL: return "a required pointer is NULL";
+    case FP_ERR_SHAPE: return "shape out of range or inconsistent (M, N, K, n_q, n_k)";
+    case FP_ERR_STRIDE: return "row stride smaller than the row length";
+    case FP_ERR_LAUNCH: return "HIP kernel launch failed";
+    case FP_ERR_DEVICE: return "no gfx950 code object for the current device";
+    default: return "unknown fp_status";
+  }
+}
+
+int fp_abi_version(void) { return (1 << 16) | 0; }
+
+int fp_qkv_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                int64_t M, int64_t n_q, int64_t n_k, int64_t K, void* stream) {
+  if (n_q < 1 || n_k < 0) return FP_ERR_SHAPE;
+  const int64_t N = n_q + 2 * n_k;
+  int st = fp::check_common(M, N, K, ldx, ldy);
+  if (st) return st;
+  if (ldw < K) return FP_ERR_STRIDE;
+  if (M == 0) return FP_OK;
+  if (!x || !w || !y) return FP_ERR_NULL;
+  StreamArgs a{(const uint16_t*)x, ldx, w, ldw, nullptr, 0, nullptr, nullptr,
+               (uint16_t*)y, ldy, M, N, K};
+  const bool aligned = (K % 8 == 0) && (ldx % 8 == 0) && (ldw % 8 == 0) &&
+                       fp::al16(x) && fp::al16(w);
+  return fp::run<false, false>(a, aligned, (hipStream_t)stream);
+}
+
+int fp_gate_up_silu_bf16(const void* x, int64_t ldx, const void* wg, int64_t ldwg,
+                         const void* wu, int64_t ldwu, void* y, int64_t ldy,
+                         int64_t M, int64_t N, int64_t K, void* stream) {
+  int st = fp::check_common(M, N, K, ldx, ldy);
+  if (st) return st;
+  if (ldwg < K || ldwu < K) return FP_ERR_STRIDE;
+  if (M == 0) return FP_OK;
+  if (!x || !wg || !wu || !y) return FP_ERR_NULL;
+  StreamArgs a{(const uint16_t*)x, ldx, wg, ldwg, wu, ldwu, nullptr, nullptr,
+               (uint16_t*)y, ldy, M, N, K};
+  const bool aligned = (K % 8 == 0) && (ldx % 8 == 0) && (ldwg % 8 == 0) && (ldwu % 8 == 0) &&
+                       fp::al16(x) && fp::al16(wg) && fp::al16(wu);
+  return fp::run<true, false>(a, aligned, (hipStream_t)stream);
+}
+
+int fp_qkv_w8(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,
+              void* y, int64_t ldy, int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+              void* stream) {
+  if (n_q < 1 || n_k < 0) return FP_ERR_SHAPE;
+  const int64_t N = n_q + 2 * n_k;
+  int st = fp::check_common(M, N, K, ldx, ldy);
+  if (st) return st;
+  if (ldq < K) return FP_ERR_STRIDE;
+  if (M == 0) return FP_OK;
+  if (!x || !q || !scale || !y) return FP_ERR_NULL;
+  StreamArgs a{(const uint16_t*)x, ldx, q, ldq, nullptr, 0, scale, nullptr,
+               (uint16_t*)y, ldy, M, N, K};
+  const bool aligned = (K % 16 == 0) && (ldx % 8 == 0) && (ldq % 16 == 0) &&
+                       fp::al16(x) && fp::al16(q);
+  return fp::run<false, true>(a, aligned, (hipStream_t)stream);
+}
+
+int fp_gate_up_silu_w8(const void* x, int64_t ldx, const int8_t* qg, int64_t ldqg,
+                       const float* sg, const int8_t* qu, int64_t ldqu, const float* su,
+                       void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
+  int st = fp::check_common(M, N, K, ldx, ldy);
+  if (st) return st;
+  if (ldqg < K || ldqu < K) return FP_ERR_STRIDE;
+  if (M == 0) return FP_OK;
+  if (!x || !qg || !sg || !qu || !su || !y) return FP_ERR_NULL;
+  StreamArgs a{(const uint16_t*)x, ldx, qg, ldqg, qu, ldqu, sg, su,
+               (uint16_t*)y, ldy, M, N, K};
+  const bool aligned = (K % 16 == 0) && (ldx % 8 == 0) && (ldqg % 16 == 0) &&
+                       (ldqu % 16 == 0) && fp::al16(x) && fp::al16(qg) && fp::al16(qu);
+  return fp::run<true, true>(a, aligned, (hipStream_t)stream);
+}
+
+int fp_quantize_w8_per_row(const void* w, int64_t ldw, int8_t* q, int64_t ldq, float* scale,
+                           int64_t N, int64_t K, void* stream) {
+  if (N < 0 || K < 1 || N > ((int64_t)1 << 31) - 1) return FP_ERR_SHAPE;
+  if (ldw < K || ldq < K) return FP_ERR_STRIDE;
+  if (N == 0) return FP_OK;
+  if (!w || !q || !scale) return FP_ERR_NULL;
+  hipLaunchKernelGGL(fp::quantize_w8_kernel, dim3((unsigned)N), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)w, ldw, q, ldq, scale, K);
+  return fp::launch_status((int)hipGetLastError());
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+// fp_common.h — shared device types and helpers for the gfx950 fused
+// projection kernels (wave64, MFMA bf16, 16-byte vector memory).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fp {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr int kWave = 64;
+
+// ---- bf16 <-> fp32, round-to-nearest-even (torch's c10::BFloat16 rule) ----
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN -> canonical qNaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+// Two fp32 -> one dword of packed bf16 (lo in bits 0..15), RNE.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// ---- epilogues -------------------------------------------------------------
+
+// silu(g) * u with the rounding points of the unfused bf16 torch path:
+// g, u are rounded to bf16 (F.linear output), silu is evaluated in fp32 on the
+// rounded g and rounded (F.silu output), the product is taken in fp32 on the
+// two bf16 operands and rounded (the elementwise mul output).
+__device__ __forceinline__ uint32_t gate_up_silu_bits(float acc_g, float acc_u) {
+  const float g = round_bf16(acc_g);
+  const float u = round_bf16(acc_u);
+  const float s = round_bf16(g / (1.0f + expf(-g)));
+  return f32_to_bf16_bits(s * u);
+}
+
+// ---- memory ---------------------------------------------------------------
+
+// 16-byte global load (global_load_dwordx4). p must be 16-byte aligned.
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Eight bf16 starting at element k of a row of length K, zero beyond K.
+// ALIGNED: the row base is 16-byte aligned and K % 8 == 0, so a chunk of eight
+// starting at a multiple of 8 lies wholly inside or wholly outside the row.
+template <bool ALIGNED>
+__device__ __forceinline__ u32x4 load_bf16x8(const uint16_t* row, int64_t k, int64_t K) {
+  if constexpr (ALIGNED) {
+    if (k < K) return ld16(row + k);
+    return u32x4{0u, 0u, 0u, 0u};
+  } else {
+    uint32_t h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (k + e < K) ? (uint32_t)row[k + e] : 0u;
+    return u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                 h[6] | (h[7] << 16)};
+  }
+}
+
+// Sixteen int8 starting at element k of a row of length K, zero beyond K.
+// ALIGNED: the row base is 16-byte aligned and K % 16 == 0.
+template <bool ALIGNED>
+__device__ __forceinline__ u32x4 load_i8x16(const int8_t* row, int64_t k, int64_t K) {
+  if constexpr (ALIGNED) {
+    if (k < K) return ld16(row + k);
+    return u32x4{0u, 0u, 0u, 0u};
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int64_t kk = k + 4 * d + b;
+        const uint32_t byte = (kk < K) ? (uint32_t)(uint8_t)row[kk] : 0u;
+        v |= byte << (8 * b);
+      }
+      w[d] = v;
+    }
+    return u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// ---- int8 -> bf16 dequantisation ------------------------------------------
+//
+// w = bf16_rne(fp32(q * s)), bit-identical to (q.float() * s).to(bfloat16):
+// the byte is biased to u = q + 128 (xor 0x80), converted exactly with
+// v_cvt_f32_ubyteN, and fma(u, s, -128 s) rounds the exact value q*s once
+// (-128 s is exact), which is the single fp32 rounding of q.float() * s.
+__device__ __forceinline__ void dequant4(uint32_t qword, float s, float neg128s,
+                                         float out[4]) {
+  const uint32_t u = qword ^ 0x80808080u;
+  // (float)(byte n of u) is selected as v_cvt_f32_ubyteN.
+  out[0] = fmaf((float)(u & 0xffu), s, neg128s);
+  out[1] = fmaf((float)((u >> 8) & 0xffu), s, neg128s);
+  out[2] = fmaf((float)((u >> 16) & 0xffu), s, neg128s);
+  out[3] = fmaf((float)(u >> 24), s, neg128s);
+}
+
+// 8 int8 (two dwords) -> 8 bf16 packed in 4 dwords.
+__device__ __forceinline__ u32x4 dequant8(uint32_t q0, uint32_t q1, float s, float neg128s) {
+  float a[4], b[4];
+  dequant4(q0, s, neg128s, a);
+  dequant4(q1, s, neg128s, b);
+  return u32x4{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]),
+               pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3])};
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// D(16x16, fp32) += A(16x32) * B(32x16), bf16 operands (gfx950 v_mfma_f32_16x16x32_bf16).
+// Lane l supplies A row (l % 16) and B column (l % 16), 8 consecutive k of the
+// 32-wide k-block selected by (l / 16); D lane l holds rows 4*(l/16)+r, col l%16.
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+}  // namespace fp

@@ -1,0 +1,41 @@
+// fp_launch.h — argument blocks and launcher declarations shared between the
+// kernel translation units and the C-ABI dispatch (fp_api.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fp {
+
+// One fused projection call. Weights are [N, K] row-major; for gate-up w0/w1
+// are Wg/Wu (s0/s1 their int8 row scales), for QKV only w0/s0 are used.
+// Strides are in elements of the respective buffer.
+struct StreamArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const void* w0;
+  int64_t ldw0;
+  const void* w1;
+  int64_t ldw1;
+  const float* s0;
+  const float* s1;
+  uint16_t* y;
+  int64_t ldy;
+  int64_t M, N, K;
+};
+
+// Weight-streaming kernels (M <= 64). Return the launch's hipError_t.
+template <bool GATEUP, bool W8>
+int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s);
+
+// LDS-tiled MFMA kernels (M > 64). Return the launch's hipError_t.
+template <bool GATEUP, bool W8>
+int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s);
+
+// Device-side per-row int8 quantisation.
+int launch_quantize_w8(const uint16_t* w, int64_t ldw, int8_t* q, int64_t ldq,
+                       float* scale, int64_t N, int64_t K, hipStream_t s);
+
+constexpr int64_t kStreamMaxM = 64;
+
+}  // namespace fp

@@ -1,0 +1,123 @@
+// torch_ops.cpp — the thin PyTorch-ROCm custom ops over the C ABI of
+// include/llms_amd_fp.h. Each op allocates its output with torch on the
+// tensor's device, takes torch's current HIP stream, and hands plain pointers,
+// row strides and sizes to the C ABI; a nonzero fp_status becomes a
+// c10::Error (RuntimeError in Python). No computation happens here.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "llms_amd_fp.h"
+
+namespace {
+
+void check_status(int st, const char* fn) {
+  TORCH_CHECK(st == FP_OK, fn, " failed: ", fp_status_string(st), " (fp_status ", st, ")");
+}
+
+void check_2d(const at::Tensor& t, const char* name, at::ScalarType dt) {
+  TORCH_CHECK(t.dim() == 2, name, " must be 2-D, got ", t.dim(), "-D");
+  TORCH_CHECK(t.scalar_type() == dt, name, " must be ", c10::toString(dt), ", got ",
+              c10::toString(t.scalar_type()));
+  TORCH_CHECK(t.size(1) <= 1 || t.stride(1) == 1, name, " must have unit inner stride");
+  TORCH_CHECK(t.is_cuda(), name, " must be a HIP device tensor");
+}
+
+void* cur_stream(const at::Tensor& t) {
+  return (void*)c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+at::Tensor qkv(const at::Tensor& x, const at::Tensor& w, int64_t n_q, int64_t n_k) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(w, "W_qkv", at::kBFloat16);
+  const c10::DeviceGuard guard(x.device());
+  const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
+  at::Tensor y = at::empty({M, N}, x.options());
+  check_status(fp_qkv_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
+                           y.stride(0), M, n_q, n_k, K, cur_stream(x)),
+               "fp_qkv_bf16");
+  return y;
+}
+
+at::Tensor gate_up_silu(const at::Tensor& x, const at::Tensor& wg, const at::Tensor& wu) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(wg, "Wg", at::kBFloat16);
+  check_2d(wu, "Wu", at::kBFloat16);
+  const c10::DeviceGuard guard(x.device());
+  const int64_t M = x.size(0), K = x.size(1), N = wg.size(0);
+  at::Tensor y = at::empty({M, N}, x.options());
+  check_status(fp_gate_up_silu_bf16(x.data_ptr(), x.stride(0), wg.data_ptr(), wg.stride(0),
+                                    wu.data_ptr(), wu.stride(0), y.data_ptr(), y.stride(0), M, N,
+                                    K, cur_stream(x)),
+               "fp_gate_up_silu_bf16");
+  return y;
+}
+
+at::Tensor qkv_w8(const at::Tensor& x, const at::Tensor& q, const at::Tensor& s, int64_t n_q,
+                  int64_t n_k) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(q, "q", at::kChar);
+  TORCH_CHECK(s.dim() == 1 && s.scalar_type() == at::kFloat && s.is_contiguous(),
+              "scale must be a contiguous 1-D float32 tensor");
+  TORCH_CHECK(s.size(0) == q.size(0), "scale has ", s.size(0), " rows, q has ", q.size(0));
+  const c10::DeviceGuard guard(x.device());
+  const int64_t M = x.size(0), K = x.size(1), N = q.size(0);
+  at::Tensor y = at::empty({M, N}, x.options());
+  check_status(fp_qkv_w8(x.data_ptr(), x.stride(0), (const int8_t*)q.data_ptr(), q.stride(0),
+                         s.data_ptr<float>(), y.data_ptr(), y.stride(0), M, n_q, n_k, K,
+                         cur_stream(x)),
+               "fp_qkv_w8");
+  return y;
+}
+
+at::Tensor gate_up_silu_w8(const at::Tensor& x, const at::Tensor& qg, const at::Tensor& sg,
+                           const at::Tensor& qu, const at::Tensor& su) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(qg, "qg", at::kChar);
+  check_2d(qu, "qu", at::kChar);
+  for (const at::Tensor* s : {&sg, &su})
+    TORCH_CHECK(s->dim() == 1 && s->scalar_type() == at::kFloat && s->is_contiguous() &&
+                    s->size(0) == qg.size(0),
+                "scales must be contiguous 1-D float32 tensors with one entry per row");
+  const c10::DeviceGuard guard(x.device());
+  const int64_t M = x.size(0), K = x.size(1), N = qg.size(0);
+  at::Tensor y = at::empty({M, N}, x.options());
+  check_status(fp_gate_up_silu_w8(x.data_ptr(), x.stride(0), (const int8_t*)qg.data_ptr(),
+                                  qg.stride(0), sg.data_ptr<float>(),
+                                  (const int8_t*)qu.data_ptr(), qu.stride(0),
+                                  su.data_ptr<float>(), y.data_ptr(), y.stride(0), M, N, K,
+                                  cur_stream(x)),
+               "fp_gate_up_silu_w8");
+  return y;
+}
+
+std::tuple<at::Tensor, at::Tensor> quantize_w8(const at::Tensor& w) {
+  check_2d(w, "W", at::kBFloat16);
+  const c10::DeviceGuard guard(w.device());
+  const int64_t N = w.size(0), K = w.size(1);
+  at::Tensor q = at::empty({N, K}, w.options().dtype(at::kChar));
+  at::Tensor s = at::empty({N}, w.options().dtype(at::kFloat));
+  check_status(fp_quantize_w8_per_row(w.data_ptr(), w.stride(0), (int8_t*)q.data_ptr(),
+                                      q.stride(0), s.data_ptr<float>(), N, K, cur_stream(w)),
+               "fp_quantize_w8_per_row");
+  return {q, s};
+}
+
+}  // namespace
+
+TORCH_LIBRARY(llms_amd, m) {
+  m.def("qkv(Tensor x, Tensor w_qkv, int n_q, int n_k) -> Tensor");
+  m.def("gate_up_silu(Tensor x, Tensor wg, Tensor wu) -> Tensor");
+  m.def("qkv_w8(Tensor x, Tensor q, Tensor scale, int n_q, int n_k) -> Tensor");
+  m.def("gate_up_silu_w8(Tensor x, Tensor qg, Tensor sg, Tensor qu, Tensor su) -> Tensor");
+  m.def("quantize_w8(Tensor w) -> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(llms_amd, CUDA, m) {
+  m.impl("qkv", qkv);
+  m.impl("gate_up_silu", gate_up_silu);
+  m.impl("qkv_w8", qkv_w8);
+  m.impl("gate_up_silu_w8", gate_up_silu_w8);
+  m.impl("quantize_w8", quantize_w8);
+}

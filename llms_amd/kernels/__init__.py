@@ -1,0 +1,25 @@
+"""Fused projection kernels for the Qwen3 engine, MI355X-native.
+
+Same import surface as the reference's ``src/kernels/__init__.py:3-14``, plus
+the int8 weight-only variants.
+"""
+
+from .fused_ffn import TritonFFN, fused_gate_up_silu, fused_gate_up_silu_w8, triton_fused_gate_up_silu
+from .fused_qkv import TritonAttention, fused_qkv, fused_qkv_w8, triton_fused_qkv
+from .quant import dequantize_w8, quantize_w8_per_row
+from .swap import apply_triton_kernels, prewarm_triton_kernels
+
+__all__ = [
+    "TritonAttention",
+    "TritonFFN",
+    "apply_triton_kernels",
+    "prewarm_triton_kernels",
+    "triton_fused_gate_up_silu",
+    "triton_fused_qkv",
+    "fused_qkv",
+    "fused_gate_up_silu",
+    "fused_qkv_w8",
+    "fused_gate_up_silu_w8",
+    "quantize_w8_per_row",
+    "dequantize_w8",
+]

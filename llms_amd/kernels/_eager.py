@@ -1,0 +1,53 @@
+"""The eager (non-projection) pieces the attention forward needs.
+
+Plain torch restatements of the Qwen3 attention neighbours of the fused QKV
+projection — RMSNorm with fp32 statistics (``src/engine/attention.py:20-33``)
+and rotate-half RoPE (``src/engine/attention.py:36-76``). They are not on the
+fused path; ``TritonAttention`` applies them after the projection exactly as
+the reference's forward does.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+
+class RMSNorm(nn.Module):
+    """y = weight * (x / sqrt(mean(x^2) + eps)), statistics in fp32, the
+    normalised value cast back to x.dtype before the weight multiply."""
+
+    def __init__(self, dim: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        inv = torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + self.eps)
+        return self.weight * (xf * inv).to(x.dtype)
+
+
+def build_rope_tables(head_dim: int, max_pos: int, base: float, *,
+                      device: torch.device | str = "cpu",
+                      dtype: torch.dtype = torch.float32) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin tables [max_pos, head_dim]; the two halves of head_dim share
+    frequencies base^(-2i/head_dim) (rotate-half convention)."""
+    exps = torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim
+    inv_freq = base ** (-exps)
+    pos = torch.arange(max_pos, dtype=torch.float32, device=device)
+    ang = pos[:, None] * inv_freq[None, :]
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos().to(dtype), ang.sin().to(dtype)
+
+
+def rotate_half(t: torch.Tensor) -> torch.Tensor:
+    h = t.shape[-1] // 2
+    return torch.cat((-t[..., h:], t[..., :h]), dim=-1)
+
+
+def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """q, k [B, H, T, D]; cos, sin [T, D]."""
+    c = cos[None, None]
+    s = sin[None, None]
+    return q * c + rotate_half(q) * s, k * c + rotate_half(k) * s

@@ -1,0 +1,320 @@
+"""GPU parity of the fused projections against the CPU oracle.
+
+Mirrors the reference's kernel test ladder (tests/test_kernels_fused_ffn.py
+and tests/test_kernels_fused_qkv.py: small bf16 shapes, Qwen3-4B shapes, N and
+K tails, leading dims, head views, error messages) and adds the task's
+configurations: Qwen3-0.6B decode, Qwen3-4B decode/spec-verify and prefill,
+int8 weight-only, and the Qwen3-8B M sweep.
+
+The bar (``oracle.ref.check_parity``): every output element within 2e-2 of
+the oracle's admissible-rounding hull, rel-L2 <= 5e-3 against the oracle's
+exact-rounding value. For large M a seeded subset of rows is checked (each
+output row depends only on its own x row); size-independent properties
+(determinism, row-permutation equivariance) run at full size.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref
+from tests._util import bits, ffn_inputs, gen, qkv_inputs, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+# Qwen3 layer shapes: (K, n_q, n_k, I)
+QWEN3_0_6B = (1024, 2048, 1024, 3072)
+QWEN3_4B = (2560, 4096, 1024, 9728)
+QWEN3_8B = (4096, 4096, 1024, 12288)
+
+
+def _kernels():
+    from llms_amd import kernels
+
+    return kernels
+
+
+def _rows(M: int, limit: int = 192, seed: int = 0) -> np.ndarray:
+    if M <= limit:
+        return np.arange(M)
+    r = np.random.default_rng(seed).choice(M, size=limit, replace=False)
+    return np.sort(np.concatenate([r, [0, M - 1]]))
+
+
+def _check(kernel_out: torch.Tensor, oracle_out: ref.OracleOut, label: str) -> ref.Parity:
+    p = ref.check_parity(bits(kernel_out), oracle_out)
+    print(f"{label}: {p}")
+    assert p.ok, f"{label}: {p}"
+    return p
+
+
+def run_qkv(x, w, n_q, n_k):
+    q, k, v = _kernels().triton_fused_qkv(x.to(DEV), w.to(DEV), n_q=n_q, n_k=n_k)
+    return torch.cat([q, k, v], dim=-1).cpu()
+
+
+def check_qkv(seed, M, K, n_q, n_k, w_std=0.02, label=""):
+    x, w = qkv_inputs(seed, M, K, n_q, n_k, w_std=w_std)
+    y = run_qkv(x, w, n_q, n_k)
+    rows = _rows(M)
+    out = ref.ref_qkv_full(bits(x)[rows], bits(w), n_q, n_k)
+    return _check(y[rows], out, label or f"qkv M={M} K={K} n_q={n_q} n_k={n_k}")
+
+
+def check_ffn(seed, M, K, N, w_std=0.02, label=""):
+    x, wg, wu = ffn_inputs(seed, M, K, N, w_std=w_std)
+    y = _kernels().triton_fused_gate_up_silu(x.to(DEV), wg.to(DEV), wu.to(DEV)).cpu()
+    rows = _rows(M)
+    out = ref.ref_gate_up_silu_full(bits(x)[rows], bits(wg), bits(wu))
+    return _check(y[rows], out, label or f"gate-up M={M} K={K} N={N}")
+
+
+# ----- reference step 2: small bf16 shapes (weights N(0,1), as there) --------
+
+
+@pytest.mark.parametrize("M,n_q,n_k,K", [(1, 128, 64, 192), (2, 128, 64, 192), (3, 160, 32, 192)])
+def test_qkv_small(M, n_q, n_k, K):
+    x, w = qkv_inputs(0, M, K, n_q, n_k, w_std=1.0)
+    y = run_qkv(x, w, n_q, n_k)
+    _check(y, ref.ref_qkv_full(bits(x), bits(w), n_q, n_k), f"qkv small {M},{n_q},{n_k},{K}")
+    # the reference's own envelope: max|a-e| < 1e-2 * max|e| + 1e-2
+    e = ref.ref_qkv_full(bits(x), bits(w), n_q, n_k).central
+    assert np.abs(y.float().numpy() - e).max() < 1e-2 * np.abs(e).max() + 1e-2
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (2, 128, 128), (3, 160, 192)])
+def test_gate_up_small(M, N, K):
+    x, wg, wu = ffn_inputs(0, M, K, N, w_std=1.0)
+    y = _kernels().triton_fused_gate_up_silu(x.to(DEV), wg.to(DEV), wu.to(DEV)).cpu()
+    out = ref.ref_gate_up_silu_full(bits(x), bits(wg), bits(wu))
+    _check(y, out, f"gate-up small {M},{N},{K}")
+    e = out.central
+    assert np.abs(y.float().numpy() - e).max() < 1e-2 * np.abs(e).max() + 1e-2
+
+
+# ----- Qwen3-0.6B decode ----------------------------------
+
+
+def test_qwen3_0_6b_decode():
+    K, n_q, n_k, I = QWEN3_0_6B
+    check_qkv(0, 1, K, n_q, n_k, label="0.6B qkv M=1")
+    check_ffn(0, 1, K, I, label="0.6B gate-up M=1")
+
+
+# ----- reference step 3 + BASELINE config 1: Qwen3-4B decode / spec-verify ---
+
+
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 8])
+def test_qwen3_4b_qkv_decode(M):
+    K, n_q, n_k, _ = QWEN3_4B
+    check_qkv(M, M, K, n_q, n_k)
+
+
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 8])
+def test_qwen3_4b_gate_up_decode(M):
+    K, _, _, I = QWEN3_4B
+    check_ffn(M, M, K, I)
+
+
+def test_gate_up_non_pow2_N():
+    """N-tail: N=9700 (reference test_triton_bf16_non_pow2_N), and a tile-tail
+    N for the prefill kernel."""
+    check_ffn(1, 1, 2560, 9700, label="gate-up N=9700 M=1")
+    check_ffn(1, 300, 2560, 9700, label="gate-up N=9700 M=300")
+    check_ffn(2, 65, 256, 37, label="gate-up N=37 M=65")
+
+
+def test_qkv_non_pow2_K():
+    """K-tail: K=2541 (reference test_triton_qkv_bf16_non_pow2_K): rows are
+    only 2-byte aligned, so the unaligned load path runs."""
+    check_qkv(1, 1, 2541, 4096, 1024, label="qkv K=2541 M=1")
+    check_qkv(1, 7, 2541, 4096, 1024, label="qkv K=2541 M=7")
+    check_qkv(1, 130, 2541, 512, 128, label="qkv K=2541 M=130")
+    check_ffn(3, 3, 2536, 512, label="gate-up K=2536 (K % 32 != 0) M=3")
+    check_ffn(3, 100, 2536, 512, label="gate-up K=2536 M=100")
+
+
+def test_preserves_leading_dims_and_head_views():
+    K = _kernels()
+    g = gen(2)
+    x = randn_bf16(g, 2, 3, 64).to(DEV)
+    wg = randn_bf16(g, 128, 64, std=0.1).to(DEV)
+    wu = randn_bf16(g, 128, 64, std=0.1).to(DEV)
+    y = K.triton_fused_gate_up_silu(x, wg, wu)
+    assert y.shape == (2, 3, 128)
+    out = ref.ref_gate_up_silu_full(bits(x), bits(wg), bits(wu))
+    _check(y.cpu(), out, "gate-up (2,3,64)")
+
+    B, T, H, Hkv, D, Kd = 1, 5, 32, 8, 128, 2560
+    x = randn_bf16(gen(3), B, T, Kd).to(DEV)
+    w = randn_bf16(gen(4), (H + 2 * Hkv) * D, Kd, std=0.02).to(DEV)
+    q, k, v = K.triton_fused_qkv(x, w, n_q=H * D, n_k=Hkv * D)
+    assert q.shape == (B, T, H * D) and k.shape == (B, T, Hkv * D) and v.shape == (B, T, Hkv * D)
+    assert q.view(B, T, H, D).shape == (B, T, H, D)
+    assert k.view(B, T, Hkv, D).shape == (B, T, Hkv, D)
+    assert v.view(B, T, Hkv, D).shape == (B, T, Hkv, D)
+    # zero-copy split: the three are views of one buffer
+    assert q.untyped_storage().data_ptr() == v.untyped_storage().data_ptr()
+
+
+def test_strided_x_and_empty_input():
+    K = _kernels()
+    g = gen(5)
+    base = randn_bf16(g, 6, 2 * 256).to(DEV)
+    x = base[:, :256]  # row stride 512, inner stride 1
+    wg = randn_bf16(g, 96, 256, std=0.05).to(DEV)
+    wu = randn_bf16(g, 96, 256, std=0.05).to(DEV)
+    y = K.triton_fused_gate_up_silu(x, wg, wu).cpu()
+    _check(y, ref.ref_gate_up_silu_full(bits(x.contiguous()), bits(wg), bits(wu)), "strided x")
+    xt = randn_bf16(g, 256, 6).to(DEV).t()  # inner stride != 1 -> copied
+    y = K.triton_fused_gate_up_silu(xt, wg, wu).cpu()
+    _check(y, ref.ref_gate_up_silu_full(bits(xt.contiguous()), bits(wg), bits(wu)), "transposed x")
+    e = torch.zeros(0, 256, dtype=torch.bfloat16, device=DEV)
+    assert K.triton_fused_gate_up_silu(e, wg, wu).shape == (0, 96)
+    w = torch.cat([wg, wu])
+    q, k, v = K.triton_fused_qkv(e, w, n_q=128, n_k=32)
+    assert q.shape == (0, 128) and k.shape == (0, 32)
+
+
+def test_dtype_and_device_errors():
+    K = _kernels()
+    x = torch.randn(2, 64, device=DEV)
+    w = torch.randn(96, 64, device=DEV)
+    with pytest.raises(TypeError, match="bfloat16"):
+        K.triton_fused_qkv(x, w, n_q=64, n_k=16)
+    xb = x.to(torch.bfloat16)
+    with pytest.raises(ValueError, match="same device"):
+        K.triton_fused_qkv(xb, w.to(torch.bfloat16).cpu(), n_q=64, n_k=16)
+
+
+# ----- Qwen3-4B prefill (MFMA regime) ---------------------
+
+
+@pytest.mark.parametrize("M", [512, 2048])
+def test_qwen3_4b_prefill(M):
+    K, n_q, n_k, I = QWEN3_4B
+    check_qkv(10 + M, M, K, n_q, n_k, label=f"4B qkv M={M}")
+    check_ffn(10 + M, M, K, I, label=f"4B gate-up M={M}")
+
+
+def test_qwen3_4b_prefill_8192_rows():
+    K, n_q, n_k, I = QWEN3_4B
+    check_qkv(8192, 8192, K, n_q, n_k, label="4B qkv M=8192 (row subset)")
+    check_ffn(8192, 8192, K, I, label="4B gate-up M=8192 (row subset)")
+
+
+@pytest.mark.parametrize("M", [17, 64, 65, 100, 256])
+def test_regime_boundaries(M):
+    """Around the streaming / tiled switch and partial M tiles."""
+    check_qkv(20 + M, M, 1024, 512, 128)
+    check_ffn(20 + M, M, 1024, 640)
+
+
+# ----- int8 weight-only -----------------------------------
+
+
+def _quant(w):
+    q, s = _kernels().quantize_w8_per_row(w.to(DEV))
+    qo, so = ref.quantize_w8_per_row(bits(w))
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)   # device packing == oracle, bit-exact
+    np.testing.assert_array_equal(s.cpu().numpy(), so)
+    return q, s
+
+
+@pytest.mark.parametrize("M", [1, 4, 2048])
+def test_qwen3_4b_int8(M):
+    K, n_q, n_k, I = QWEN3_4B
+    kern = _kernels()
+    x, w = qkv_inputs(30 + M, M, K, n_q, n_k)
+    q, s = _quant(w)
+    yq, yk, yv = kern.fused_qkv_w8(x.to(DEV), q, s, n_q=n_q, n_k=n_k)
+    y = torch.cat([yq, yk, yv], -1).cpu()
+    rows = _rows(M)
+    out = ref.ref_qkv_w8_full(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy(), n_q, n_k)
+    _check(y[rows], out, f"4B int8 qkv M={M}")
+
+    x, wg, wu = ffn_inputs(40 + M, M, K, I)
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+    out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                       qu.cpu().numpy(), su.cpu().numpy())
+    _check(y[rows], out, f"4B int8 gate-up M={M}")
+
+
+def test_int8_tails_and_zero_rows():
+    kern = _kernels()
+    for M, K, N in [(3, 2541, 100), (70, 2541, 100), (5, 1040, 48), (90, 1040, 48)]:
+        x, wg, wu = ffn_inputs(M + K, M, K, N)
+        wg[3] = 0  # an all-zero row: s = 0, q = 0
+        qg, sg = _quant(wg)
+        qu, su = _quant(wu)
+        y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+        out = ref.ref_gate_up_silu_w8_full(bits(x), qg.cpu().numpy(), sg.cpu().numpy(),
+                                           qu.cpu().numpy(), su.cpu().numpy())
+        _check(y, out, f"int8 gate-up M={M} K={K} N={N}")
+
+
+# ----- Qwen3-8B M sweep, bf16 and int8 ---------------------
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 64, 256, 4096])
+def test_qwen3_8b_sweep(M):
+    K, n_q, n_k, I = QWEN3_8B
+    check_qkv(50 + M, M, K, n_q, n_k, label=f"8B qkv M={M}")
+    check_ffn(50 + M, M, K, I, label=f"8B gate-up M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 16, 256])
+def test_qwen3_8b_int8(M):
+    K, _, _, I = QWEN3_8B
+    x, wg, wu = ffn_inputs(60 + M, M, K, I)
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    y = _kernels().fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+    rows = _rows(M)
+    out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                       qu.cpu().numpy(), su.cpu().numpy())
+    _check(y[rows], out, f"8B int8 gate-up M={M}")
+
+
+# ----- size-independent properties at full size ------------------------------
+
+
+@pytest.mark.parametrize("M", [1, 8, 2048])
+def test_deterministic_and_row_permutation_equivariant(M):
+    """Repeated calls are bit-identical (the reference's prewarm test demands
+    diff == 0.0), and permuting weight rows permutes output columns exactly."""
+    K, _, _, I = QWEN3_4B
+    kern = _kernels()
+    x, wg, wu = ffn_inputs(70 + M, M, K, I)
+    x, wg, wu = x.to(DEV), wg.to(DEV), wu.to(DEV)
+    y1 = kern.triton_fused_gate_up_silu(x, wg, wu)
+    y2 = kern.triton_fused_gate_up_silu(x, wg, wu)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    perm = torch.randperm(I, generator=gen(M)).to(DEV)
+    yp = kern.triton_fused_gate_up_silu(x, wg[perm].contiguous(), wu[perm].contiguous())
+    assert torch.equal(yp.view(torch.int16), y1[:, perm].view(torch.int16))
+
+
+def test_against_torch_gpu_path():
+    """Report-only comparison with the reference's unfused path on the same
+    device (hipBLASLt F.linear + F.silu): both must sit inside the oracle hull
+    with the same tolerance."""
+    import torch.nn.functional as F
+
+    K, n_q, n_k, I = QWEN3_4B
+    for M in (1, 8, 512):
+        x, wg, wu = ffn_inputs(80 + M, M, K, I)
+        xd, gd, ud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+        ours = _kernels().triton_fused_gate_up_silu(xd, gd, ud).cpu()
+        theirs = (F.silu(F.linear(xd, gd)) * F.linear(xd, ud)).cpu()
+        out = ref.ref_gate_up_silu_full(bits(x), bits(wg), bits(wu))
+        p_ours = ref.check_parity(bits(ours), out)
+        p_theirs = ref.check_parity(bits(theirs), out)
+        print(f"M={M} ours: {p_ours}\nM={M} torch-gpu: {p_theirs}")
+        assert p_ours.ok
