@@ -8,7 +8,7 @@ set of Qwen3-4B is far above the 256 MB Infinity Cache. Inputs x ~ N(0, 1)
 are resident in HBM before timing starts. The step's 72 launches are captured
 once in a HIP graph and replayed.
 
-Headline (BASELINE.json metric): HBM GB/s at M=1 on Qwen3-4B shapes =
+Headline metric: HBM GB/s at M=1 on Qwen3-4B shapes =
 algorithmic bytes per layer pair (2K(N_qkv+2I) + 4MK + 2M(N_qkv+I)) x layers /
 step time. Also reported: TFLOP/s at M=2048 (prefill), the dominant kernel's
 roofline (per-launch HIP events on its stream), and the reference's unfused
@@ -117,20 +117,34 @@ def time_graph(torch, graph, steps: int, warmup: int) -> float:
     return t0.elapsed_time(t1) / 1e3 / steps
 
 
-def time_launches(torch, launches: list, reps: int) -> list[float]:
-    """Per-launch durations (s) from HIP event pairs recorded on the stream the
-    kernels are launched on (torch's current stream)."""
-    evs = []
-    for _ in range(reps):
-        for fn in launches:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record()
-            fn()
-            b.record()
-            evs.append((a, b))
-    torch.cuda.synchronize()
-    return [a.elapsed_time(b) / 1e3 for a, b in evs]
+def kernel_seconds(torch, launches: list, reps: int) -> float:
+    """Average duration (s) of one launch of a kernel: the launches (one per
+    layer weight set) are captured in a HIP graph, the graph is replayed
+    `reps` times between HIP events on the stream it runs on, and the elapsed
+    time is divided by the number of launches. Graph replay keeps the GPU fed
+    back-to-back, so no host launch latency is counted."""
+    graph = capture(torch, lambda: [fn() for fn in launches])
+    sec = time_graph(torch, graph, reps, 2)
+    del graph
+    return sec / len(launches)
+
+
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "stream_kernel_qwen3-4b_decode_m1.md")
+
+
+def profiled_traffic(path: str = TRAFFIC_PROFILE):
+    """HBM bytes per launch of the dominant kernel from its committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or
+    None when the summary is absent."""
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return int(ln.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(shape, M: int, sets: int, reps: int) -> dict:
@@ -186,6 +200,42 @@ def cpu_baseline(shape, M: int, sets: int, reps: int) -> dict:
     }
 
 
+def counters_run(torch, kern, shape, layers: int) -> dict:
+    """A short fixed sequence for `rocprofv3 --pmc` runs: a plain device copy
+    of known size (calibrates FETCH_SIZE / WRITE_SIZE), then the decode (M=1)
+    and prefill (M=2048) fused kernels over `layers` cycled weight sets."""
+    K, n_q, n_k, inter = shape
+    n_qkv = n_q + 2 * n_k
+    copy_bytes = 256 << 20
+    src = torch.empty(copy_bytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    stack = Stack(torch, shape, layers, M=1)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    run_step(stack, kern)
+    torch.cuda.synchronize()
+    stack.set_m(torch, 2048)
+    for l in range(min(4, layers)):
+        kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k)
+        kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l])
+    torch.cuda.synchronize()
+    return {
+        "mode": "counters",
+        "copy": {"kernel": "bfloat16_copy_kernel", "read_bytes": copy_bytes,
+                 "write_bytes": copy_bytes, "launches": 3},
+        "gate_up_m1": {"read_bytes": 2 * K * 2 * inter + 2 * K, "write_bytes": 2 * inter,
+                       "launches": layers},
+        "qkv_m1": {"read_bytes": 2 * K * n_qkv + 2 * K, "write_bytes": 2 * n_qkv,
+                   "launches": layers},
+        "gate_up_m2048": {"read_bytes": 2 * K * 2 * inter + 2 * 2048 * K,
+                          "write_bytes": 2 * 2048 * inter, "launches": min(4, layers)},
+        "qkv_m2048": {"read_bytes": 2 * K * n_qkv + 2 * 2048 * K,
+                      "write_bytes": 2 * 2048 * n_qkv, "launches": min(4, layers)},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,11 +248,13 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--counters", action="store_true",
+                    help="run only the short fixed sequence used for rocprofv3 --pmc runs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only; the fused projections shard "
-              "by output columns with no collective inside the path (see DESIGN.md). "
+              "by output columns with no collective inside the path. "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
 
@@ -220,6 +272,9 @@ def main() -> int:
     K, n_q, n_k, inter = shape
     n_qkv = n_q + 2 * n_k
     L = args.layers
+    if args.counters:
+        print(json.dumps(counters_run(torch, kern, shape, L)), flush=True)
+        return 0
 
     # ---------------- decode, M = 1: the headline ----------------
     log(f"device {dev_name}; allocating {L} layer weight sets of {args.model}")
@@ -242,14 +297,13 @@ def main() -> int:
     torch.cuda.synchronize()
     sec_eager = (time.perf_counter() - t0) / args.steps
 
-    # dominant kernel (gate-up, 76% of the bytes): per-launch HIP events
+    # dominant kernel (gate-up, 76% of the bytes) and QKV, each alone
     gu = [(lambda l=l: kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l]))
           for l in range(L)]
     qk = [(lambda l=l: kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k))
           for l in range(L)]
-    time_launches(torch, gu, 1)
-    d_gu = statistics.mean(time_launches(torch, gu, max(2, args.steps // 4)))
-    d_qk = statistics.mean(time_launches(torch, qk, max(2, args.steps // 4)))
+    d_gu = kernel_seconds(torch, gu, args.steps)
+    d_qk = kernel_seconds(torch, qk, args.steps)
     gu_gbs = gate_up_bytes(1, K, inter) / d_gu / 1e9
     qk_gbs = (2 * K * n_qkv + 2 * K + 2 * n_qkv) / d_qk / 1e9
     log(f"gate-up M=1: {d_gu * 1e6:.2f} us/launch {gu_gbs:.1f} GB/s; "
@@ -266,8 +320,8 @@ def main() -> int:
         psteps = max(3, args.steps // 4)
         psec = time_graph(torch, graph, psteps, max(1, args.warmup // 2))
         tflops = L * pair_flops(Mp, K, n_qkv, inter) / psec / 1e12
-        dp_gu = statistics.mean(time_launches(torch, gu, 2))
-        dp_qk = statistics.mean(time_launches(torch, qk, 2))
+        dp_gu = kernel_seconds(torch, gu, 3)
+        dp_qk = kernel_seconds(torch, qk, 3)
         prefill = {
             "M": Mp,
             "tflops": round(tflops, 1),
@@ -327,7 +381,9 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(),
+            "algorithmic_bytes": gate_up_bytes(1, K, inter),
+            "avg_launch_us": round(d_gu * 1e6, 3),
         },
         "prefill": prefill,
         "cpu_baseline": cpu,

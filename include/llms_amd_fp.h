@@ -88,7 +88,7 @@ int fp_gate_up_silu_bf16(const void* x, int64_t ldx,
 
 /*
  * int8 weight-only QKV (no reference counterpart: the reference names
- * weight quantisation only as future work, DESIGN.md:120).
+ * weight quantisation only as future work, reference DESIGN.md:120).
  *   q [n_q+2*n_k, K] int8 (row stride ldq), scale [n_q+2*n_k] fp32.
  */
 int fp_qkv_w8(const void* x, int64_t ldx,

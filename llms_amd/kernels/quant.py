@@ -1,7 +1,7 @@
 """Per-output-channel symmetric int8 weight packing (the swap-time step of the
 int8 weight-only projections).
 
-The reference has no int8 path (its DESIGN.md:120 lists quantisation as future
+The reference has no int8 path (reference DESIGN.md:120 lists quantisation as future
 work); the format is this build's: for each output row r of an ``[N, K]``
 weight, ``s[r] = max_k |W[r, k]| / 127`` in fp32 and
 ``q[r, k] = clamp(rint(W[r, k] / s[r]), -127, 127)`` as int8 (ties to even;

@@ -24,7 +24,7 @@ Parity status per function (each is pinned by tests/test_oracle.py):
   reference call), by exact rational brute force on tiny inputs, by closed
   forms (one-hot inputs), and by committed golden vectors.
 - ``quantize_w8_per_row``, ``dequant_w8``, ``ref_*_w8``: the reference has no
-  int8 path (its DESIGN.md:120 names quantisation as future work), so the
+  int8 path (reference DESIGN.md:120 names quantisation as future work), so the
   definition comes from the task's stated formula; pinned by closed forms
   (symmetry, the row maximum maps to +-127, all-zero rows), by a torch
   restatement, and by golden vectors.

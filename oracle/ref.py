@@ -16,7 +16,7 @@ those of the torch path the reference runs when the fused kernels are off:
   ``u = bf16(x.Wu^T)``, ``s = bf16(silu(g))`` with silu evaluated on the
   rounded g, ``y = bf16(s * u)``.
 - int8 weight-only (no reference counterpart; the reference names weight
-  quantisation as future work only, ``DESIGN.md:120``): per output row
+  quantisation as future work only, reference ``DESIGN.md:120``): per output row
   ``s_r = max|w_r| / 127`` (fp32), ``q = clamp(rint(w / s_r), -127, 127)``;
   the dequantised weight is ``bf16(fp32(q * s_r))`` and the bf16 path above
   runs on it ("dequantise then matmul").
