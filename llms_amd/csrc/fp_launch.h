@@ -32,6 +32,12 @@ int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s);
 template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s);
 
+// Direct-to-LDS bf16 MFMA contraction (fp_gemm.hip), used by launch_tiled
+// when gemm_supported() holds.
+bool gemm_supported(const StreamArgs& a, bool aligned);
+template <bool GATEUP>
+int launch_gemm(const StreamArgs& a, hipStream_t s);
+
 // Device-side per-row int8 quantisation.
 int launch_quantize_w8(const uint16_t* w, int64_t ldw, int8_t* q, int64_t ldq,
                        float* scale, int64_t N, int64_t K, hipStream_t s);

@@ -206,8 +206,11 @@ int launch_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 
 }  // namespace
 
+// bf16 calls that meet gemm_kernel's requirements run there (direct-to-LDS
+// loads, XCD-aware order); int8, unaligned rows and K tails run tiled_kernel.
 template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
+  if (!W8 && gemm_supported(a, aligned)) return launch_gemm<GATEUP>(a, s);
   return launch_cfg<128, 128, 64, 2, 2, GATEUP, W8>(a, aligned, s);
 }
 
