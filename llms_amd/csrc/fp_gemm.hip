@@ -135,21 +135,25 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Fragment addresses: sub-tile i of a wave reads tile row base + 16 i + li,
+  // and swz() of that row does not depend on i (16 i only touches row bits
+  // above the swizzle), so every fragment address is one per-lane byte offset
+  // plus the compile-time constants 16 i * 128 and the stage base. k-substep
+  // kk = 1 flips chunk bit 2 (chunk (4 + grp) ^ s = (grp ^ s) ^ 4).
+  const int ra = wn * TN + li, rb = wm * TM + li;
+  const uint32_t offa = (uint32_t)(ra * kBK * 2 + ((grp ^ swz(ra)) * 16));
+  const uint32_t offb = (uint32_t)(rb * kBK * 2 + ((grp ^ swz(rb)) * 16));
   auto compute = [&](const uint16_t (*tw)[kBK], const uint16_t (*tx)[kBK]) {
 #pragma unroll
     for (int kk = 0; kk < kBK / 32; ++kk) {
-      const int ch = kk * 4 + grp;
+      const uint32_t oa = offa ^ (uint32_t)(kk * 64), ob = offb ^ (uint32_t)(kk * 64);
       u32x4 fa[FN], fb[FM];
 #pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        const int r = wn * TN + i * 16 + li;
-        fa[i] = *reinterpret_cast<const u32x4*>(&tw[r][(ch ^ swz(r)) * 8]);
-      }
+      for (int i = 0; i < FN; ++i)
+        fa[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * kBK * 2);
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const int r = wm * TM + j * 16 + li;
-        fb[j] = *reinterpret_cast<const u32x4*>(&tx[r][(ch ^ swz(r)) * 8]);
-      }
+      for (int j = 0; j < FM; ++j)
+        fb[j] = *reinterpret_cast<const u32x4*>((const char*)tx + ob + j * 16 * kBK * 2);
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -250,12 +254,13 @@ bool gemm_supported(const StreamArgs& a, bool aligned) {
 }
 
 // Tile table for the bf16 prefill path (measured on MI355X, Qwen3-4B
-// shapes): 8 waves of 64x64; up to M = 4096 tiles of 128 weight rows x 256
-// x rows, beyond that 256 x 128.
+// shapes): 8 waves; above M = 1024 tiles of 256 weight rows x 256 x rows
+// (64 x 128 per wave), below that 128 x 256 (64 x 64 per wave) so that small
+// calls still spread over more workgroups.
 template <bool GATEUP>
 int launch_gemm(const StreamArgs& a, hipStream_t s) {
-  if (a.M <= 4096) return launch_gemm_cfg<128, 256, 2, 4, GATEUP, 2>(a, s);
-  return launch_gemm_cfg<256, 128, 4, 2, GATEUP, 2>(a, s);
+  if (a.M <= 1024) return launch_gemm_cfg<128, 256, 2, 4, GATEUP, 2>(a, s);
+  return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
 }
 
 template int launch_gemm<false>(const StreamArgs&, hipStream_t);
