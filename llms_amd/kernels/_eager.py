@@ -51,3 +51,28 @@ def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.T
     c = cos[None, None]
     s = sin[None, None]
     return q * c + rotate_half(q) * s, k * c + rotate_half(k) * s
+
+
+def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos: int) -> torch.Tensor:
+    """Causal softmax attention of queries at positions start_pos .. start_pos+T-1
+    over keys/values at positions 0 .. S-1.
+
+    q [B, H, T, D]; k, v [B, H, S, D] (GQA heads already expanded). Same
+    result as the reference's three ``scaled_dot_product_attention`` branches
+    (``src/engine/attention.py:173-181``: no mask for T == 1, ``is_causal`` at
+    start_pos 0, an explicit ``q_pos >= k_pos`` mask otherwise), which all
+    reduce to "key position <= query position" with scale D^-0.5.
+
+    The core runs in fp32 on contiguous operands and casts back to q.dtype:
+    the result then does not depend on which SDPA backend torch would pick,
+    and no bf16 batched product sees a transposed operand.
+    """
+    T, S = q.shape[2], k.shape[2]
+    scores = torch.matmul(q.float().contiguous(), k.float().transpose(-2, -1).contiguous())
+    scores = scores * (q.shape[-1] ** -0.5)
+    if T > 1:
+        q_pos = torch.arange(start_pos, start_pos + T, device=q.device)[:, None]
+        k_pos = torch.arange(S, device=q.device)[None, :]
+        scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
+    p = torch.softmax(scores, dim=-1)
+    return torch.matmul(p, v.float().contiguous()).to(q.dtype)

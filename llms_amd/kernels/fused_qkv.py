@@ -12,12 +12,11 @@ Python wrapper -> ``torch.ops.llms_amd.qkv`` -> C ABI ``fp_qkv_bf16``
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from .. import _lib
 from ._checks import inner_contiguous, require_bf16_hip, require_device
-from ._eager import RMSNorm, apply_rope
+from ._eager import RMSNorm, apply_rope, attend
 
 
 def triton_fused_qkv(
@@ -125,7 +124,9 @@ class TritonAttention(nn.Module):
     """Drop-in for the reference's ``TritonAttention``
     (``src/kernels/fused_qkv.py:152-282``): stores one stacked ``W_qkv``
     instead of ``q``/``k``/``v`` Linears and runs the fused HIP projection;
-    QK-norm, RoPE, the KV-cache write, SDPA and ``o`` stay eager.
+    QK-norm, RoPE, the KV-cache write, attention and ``o`` stay eager (the
+    attention core is :func:`attend`, fp32 softmax attention with the
+    reference's causal semantics).
 
     With ``from_eager(..., int8=True)`` the stacked weight is kept as
     per-row int8 (``q_qkv``, ``s_qkv`` buffers) and the int8 kernel runs.
@@ -203,7 +204,8 @@ class TritonAttention(nn.Module):
         start_pos: int,
     ) -> torch.Tensor:
         # The reference forward (src/kernels/fused_qkv.py:242-282) with the
-        # fused HIP projection in place of the Triton call.
+        # fused HIP projection in place of the Triton call and attend() in
+        # place of its three SDPA branches.
         B, T, _ = x.shape
         q_flat, k_flat, v_flat = self.project(x)
         q = q_flat.view(B, T, self.num_heads, self.head_dim)
@@ -226,14 +228,6 @@ class TritonAttention(nn.Module):
             full_k = full_k.repeat_interleave(n_rep, dim=1)
             full_v = full_v.repeat_interleave(n_rep, dim=1)
 
-        if T == 1:
-            attn = F.scaled_dot_product_attention(q, full_k, full_v, is_causal=False)
-        elif start_pos == 0:
-            attn = F.scaled_dot_product_attention(q, full_k, full_v, is_causal=True)
-        else:
-            q_pos = torch.arange(start_pos, end_pos, device=q.device).unsqueeze(1)
-            k_pos = torch.arange(0, end_pos, device=q.device).unsqueeze(0)
-            attn = F.scaled_dot_product_attention(q, full_k, full_v, attn_mask=q_pos >= k_pos)
-
+        attn = attend(q, full_k, full_v, start_pos)
         attn = attn.transpose(1, 2).reshape(B, T, self.num_heads * self.head_dim)
         return self.o(attn)

@@ -1,0 +1,240 @@
+"""Module-level drop-in tests: ``TritonAttention``, ``TritonFFN``,
+``apply_triton_kernels`` and ``prewarm_triton_kernels`` inside a tiny synthetic
+Qwen3 engine (``tests/_tiny_qwen3.py``).
+
+Mirrors the reference's engine-integration tests, which need network weights
+(Qwen3-0.6B) and so cannot run here; the tiny model stands in for them:
+
+- ``test_kernels_fused_ffn.py:296-336`` / ``test_kernels_fused_qkv.py:330-370``
+  (module logits match eager, last-token argmax equal),
+- ``test_kernels_fused_ffn.py:338-357`` / ``test_kernels_fused_qkv.py:373-393``
+  (``apply_triton_kernels`` idempotent),
+- ``test_kernels_fused_ffn.py:360-392`` (prewarm leaves outputs bit-identical),
+- ``test_kernels_fused_ffn.py:395-406`` (prewarm no-op without fused modules),
+- ``test_kernels_fused_ffn.py:458-503`` / ``test_kernels_fused_qkv.py:443-494``
+  (greedy generation token match).
+
+Differences, on purpose: the build is bf16-only, so the reference's fp32
+cases have no counterpart; its bf16 greedy case is ``xfail(strict=False)``
+("reductions are non-associative"), replaced here by a margin-aware check
+that must pass: along the fused model's greedy trajectory, every position
+whose eager top-1/top-2 logit margin exceeds twice the observed logit
+difference must have the same argmax.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from torch import nn
+
+from llms_amd.kernels import TritonAttention, TritonFFN, apply_triton_kernels, prewarm_triton_kernels
+from tests._tiny_qwen3 import Cfg, greedy_generate, teacher_forced_logits, tiny_model, tiny_state
+
+DEV = "cuda"
+
+# the reference fixture's shape, and a wider one whose prefill runs the MFMA
+# path (M > 64, K of several 64-wide steps, N not a multiple of any tile)
+TINY = Cfg()
+WIDE = Cfg(vocab_size=96, hidden_size=256, num_hidden_layers=3, num_attention_heads=8,
+           num_key_value_heads=2, head_dim=32, intermediate_size=384,
+           max_position_embeddings=512)
+
+PROMPTS = [
+    [1, 20, 3, 14, 5, 26, 7, 18],
+    [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12],
+    [22, 22, 22, 22, 22],
+]
+
+
+def _pair(c: Cfg, seed: int = 0, device: str = DEV, **apply_kw):
+    st = tiny_state(c, seed=seed)
+    eager = tiny_model(c, state=st, device=device)
+    fused = apply_triton_kernels(tiny_model(c, state=st, device=device), **apply_kw)
+    return eager, fused
+
+
+def _logits(model, ids: torch.Tensor, max_seq: int = 64) -> torch.Tensor:
+    with torch.inference_mode():
+        return model(ids, model.alloc_cache(max_seq))
+
+
+# ---------------------------------------------------------------- CPU only
+
+
+def test_apply_is_idempotent_and_keeps_state_keys():
+    """Swap structure on CPU (no kernel launch): the walker replaces every
+    block's modules once, a second call keeps the same objects, FFN state keys
+    stay ``gate/up/down``, attention's ``q/k/v`` become one ``W_qkv``."""
+    m = tiny_model(TINY, device="cpu")
+    eager_keys = set(m.state_dict())
+    apply_triton_kernels(m)
+    first = [(b.attn, b.ffn) for b in m.layers]
+    assert all(isinstance(a, TritonAttention) and isinstance(f, TritonFFN) for a, f in first)
+    apply_triton_kernels(m)
+    assert all(a is b.attn and f is b.ffn for (a, f), b in zip(first, m.layers, strict=True))
+
+    keys = set(m.state_dict())
+    for i in range(TINY.num_hidden_layers):
+        p = f"layers.{i}.attn."
+        assert {p + "q.weight", p + "k.weight", p + "v.weight"} <= eager_keys
+        assert not {p + "q.weight", p + "k.weight", p + "v.weight"} & keys
+        assert p + "W_qkv" in keys
+        for name in ("gate", "up", "down"):
+            assert f"layers.{i}.ffn.{name}.weight" in keys
+    # W_qkv is the row-stack [Wq; Wk; Wv]; the FFN shares the eager tensors
+    ref = tiny_model(TINY, device="cpu")
+    for b, rb in zip(m.layers, ref.layers, strict=True):
+        stacked = torch.cat([rb.attn.q.weight, rb.attn.k.weight, rb.attn.v.weight])
+        assert torch.equal(b.attn.W_qkv, stacked)
+
+
+def test_apply_respects_flags():
+    m = apply_triton_kernels(tiny_model(TINY, device="cpu"), fused_ffn=False, fused_qkv=True)
+    assert all(isinstance(b.attn, TritonAttention) for b in m.layers)
+    assert not any(isinstance(b.ffn, TritonFFN) for b in m.layers)
+    m = apply_triton_kernels(tiny_model(TINY, device="cpu"), fused_ffn=True, fused_qkv=False)
+    assert not any(isinstance(b.attn, TritonAttention) for b in m.layers)
+    assert all(isinstance(b.ffn, TritonFFN) for b in m.layers)
+
+
+def test_prewarm_no_op_without_fused_modules():
+    """Reference ``test_kernels_fused_ffn.py:395-406``: a model with no
+    fused modules (and no ``.layers``) is walked without error."""
+    prewarm_triton_kernels(nn.Sequential(nn.Linear(4, 4)))
+
+
+def test_fused_modules_refuse_cpu_tensors():
+    """The product path has no CPU fallback: the fused forward on CPU raises."""
+    m = apply_triton_kernels(tiny_model(TINY, device="cpu"))
+    with pytest.raises(ValueError):
+        _logits(m, torch.tensor([[1, 2, 3]]))
+
+
+# ---------------------------------------------------------------- GPU
+
+
+def _logit_tol(ref: torch.Tensor) -> float:
+    # a few bf16 ulps of the largest logit: the two models differ only in the
+    # projections' summation order (one-ulp flips), propagated through the
+    # residual stream
+    return 4.0 * 2.0 ** (torch.floor(torch.log2(ref.abs().max())).item() - 7)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("which", ["ffn", "qkv", "both"])
+@pytest.mark.parametrize("c", [TINY, WIDE], ids=["tiny", "wide"])
+def test_module_logits_match(which, c):
+    """Prefill logits of the swapped model agree with the eager model and the
+    last-token argmax is equal (reference ``test_ffn_module_logits_match``,
+    ``test_attention_module_logits_match``)."""
+    kw = {"ffn": dict(fused_ffn=True, fused_qkv=False),
+          "qkv": dict(fused_ffn=False, fused_qkv=True),
+          "both": dict(fused_ffn=True, fused_qkv=True)}[which]
+    eager, fused = _pair(c, **kw)
+    assert all(isinstance(b.ffn, TritonFFN) == kw["fused_ffn"] for b in fused.layers)
+    assert all(isinstance(b.attn, TritonAttention) == kw["fused_qkv"] for b in fused.layers)
+    T = 8 if c is TINY else 300  # 300 rows: the MFMA prefill path
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, c.vocab_size, (1, T), generator=g).to(DEV)
+    le = _logits(eager, ids, max_seq=T + 4).float()
+    lf = _logits(fused, ids, max_seq=T + 4).float()
+    diff = (le - lf).abs().max().item()
+    tol = _logit_tol(le)
+    print(f"\n{which} {c.hidden_size}: max |logit diff| {diff:.4f} (tol {tol:.4f})")
+    assert diff <= tol
+    assert le[0, -1].argmax().item() == lf[0, -1].argmax().item()
+
+
+@pytest.mark.gpu
+def test_apply_idempotent_on_device():
+    m = tiny_model(TINY, device=DEV)
+    apply_triton_kernels(m)
+    w = [b.attn.W_qkv for b in m.layers]
+    ffn = [b.ffn for b in m.layers]
+    apply_triton_kernels(m)
+    assert all(a is b.attn.W_qkv for a, b in zip(w, m.layers, strict=True))
+    assert all(a is b.ffn for a, b in zip(ffn, m.layers, strict=True))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("int8", [False, True], ids=["bf16", "int8"])
+def test_prewarm_runs_clean(int8):
+    """prewarm leaves forward outputs bit-identical (reference
+    ``test_prewarm_runs_clean``)."""
+    m = apply_triton_kernels(tiny_model(TINY, device=DEV), int8=int8)
+    ids = torch.tensor([[1, 20, 3, 14, 5, 26, 7, 18]], device=DEV)
+    before = _logits(m, ids, 32)
+    prewarm_triton_kernels(m)
+    prewarm_triton_kernels(m, m_values=(1, 9, 64, 65, 200))
+    after = _logits(m, ids, 32)
+    assert torch.equal(before, after)
+
+
+GREEDY_CASES = [(TINY, p) for p in PROMPTS] + [
+    (WIDE, torch.randint(0, WIDE.vocab_size, (100,), generator=torch.Generator().manual_seed(9)).tolist()),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c,prompt", GREEDY_CASES, ids=["tiny-p8", "tiny-p12", "tiny-p5", "wide-p100"])
+def test_greedy_token_match(c, prompt):
+    """Greedy generation, both kernels on (reference
+    ``test_greedy_e2e_token_match_qkv``): the fused trajectory's tokens are
+    the eager argmax wherever eager's top-2 margin is not a near-tie, the
+    eager model's own greedy run gives the same tokens up to the first
+    near-tie, and prefill + decode through the KV cache agrees with one
+    teacher-forced prefill of the same tokens. The 100-token prompt prefills
+    through the MFMA path, then decodes through the weight-streaming path."""
+    st = tiny_state(c, seed=1, embed_scale=0.05)
+    eager = tiny_model(c, state=st, device=DEV)
+    fused = apply_triton_kernels(tiny_model(c, state=st, device=DEV))
+    n_new = 32
+    toks_f = greedy_generate(fused, prompt, n_new, DEV)
+    toks_e = greedy_generate(eager, prompt, n_new, DEV)
+
+    seq = prompt + toks_f
+    le = teacher_forced_logits(eager, seq, DEV)
+    lf = teacher_forced_logits(fused, seq, DEV)
+    diff = (le - lf).abs().max().item()
+    assert diff <= _logit_tol(le)
+    pos = range(len(prompt) - 1, len(seq) - 1)  # logits that chose toks_f
+    top2 = le.topk(2, dim=-1).values
+    margin = top2[:, 0] - top2[:, 1]
+    first_tie = None
+    for i, p in enumerate(pos):
+        if margin[p].item() <= 2 * diff + 1e-6:
+            first_tie = i if first_tie is None else first_tie
+            continue
+        assert toks_f[i] == int(le[p].argmax()), f"step {i}: margin {margin[p].item():.4f}"
+    upto = n_new if first_tie is None else first_tie
+    print(f"\n{c.hidden_size} prompt[:8] {prompt[:8]}: fused {toks_f}, first near-tie {first_tie}, "
+          f"teacher-forced diff {diff:.4f}")
+    assert toks_e[:upto] == toks_f[:upto]
+    assert len(set(toks_f)) > 1 or len(set(prompt)) == 1  # a non-trivial trajectory
+
+
+@pytest.mark.gpu
+def test_int8_model_matches_dequantised_eager():
+    """``apply_triton_kernels(int8=True)``: logits match an eager model whose
+    q/k/v/gate/up weights are replaced by their dequantised bf16(q * s)."""
+    from llms_amd.kernels import dequantize_w8, quantize_w8_per_row
+
+    c = WIDE
+    st = tiny_state(c, seed=3)
+    fused = apply_triton_kernels(tiny_model(c, state=st, device=DEV), int8=True)
+    deq = dict(st)
+    for k, v in st.items():
+        if k.endswith(("attn.q.weight", "attn.k.weight", "attn.v.weight",
+                       "ffn.gate.weight", "ffn.up.weight")):
+            q, s = quantize_w8_per_row(v.to(torch.bfloat16).to(DEV))
+            deq[k] = dequantize_w8(q, s).float().cpu()
+    eager = tiny_model(c, state=deq, device=DEV)
+    for T in (1, 7, 130):
+        ids = torch.randint(0, c.vocab_size, (1, T), generator=torch.Generator().manual_seed(T))
+        le = _logits(eager, ids.to(DEV), T + 4).float()
+        lf = _logits(fused, ids.to(DEV), T + 4).float()
+        diff = (le - lf).abs().max().item()
+        print(f"\nint8 T={T}: max |logit diff| {diff:.4f}")
+        assert diff <= _logit_tol(le)
+        assert le[0, -1].argmax().item() == lf[0, -1].argmax().item()
