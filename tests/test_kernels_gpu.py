@@ -255,6 +255,18 @@ def test_regime_boundaries(M):
     check_ffn(20 + M, M, 1024, 640)
 
 
+@pytest.mark.parametrize("K,N", [(8, 5), (520, 33), (2536, 9701), (16384, 64), (16392, 24), (4096, 1)])
+def test_single_row_streaming_edges(K, N):
+    """M = 1 bf16 runs the row-streaming kernel (one wave per weight row, K in
+    512-element chunks, x in LDS up to K = 16384): tiny and ragged K (the last
+    chunk partly past the row), N not a multiple of the rows per workgroup,
+    the largest K it takes and the first K it hands to the streaming kernel."""
+    n_q = max(N - 2 * (N // 4), 1)
+    n_k = (N - n_q) // 2
+    check_qkv(40 + K, 1, K, n_q, n_k, label=f"qkv M=1 K={K} N={n_q + 2 * n_k}")
+    check_ffn(41 + K, 1, K, N, label=f"gate-up M=1 K={K} N={N}")
+
+
 # ----- int8 weight-only --------------------------------------------------------
 
 
