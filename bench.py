@@ -130,7 +130,7 @@ def kernel_seconds(torch, launches: list, reps: int) -> float:
 
 
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "stream_kernel_qwen3-4b_decode_m1.md")
+                               "rows_kernel_qwen3-4b_decode_m1.md")
 
 
 def profiled_traffic(path: str = TRAFFIC_PROFILE):
@@ -375,7 +375,7 @@ def main() -> int:
             "qkv_gbs": round(qk_gbs, 1),
         },
         "roofline": {
-            "kernel": "gate-up-SiLU bf16 M=1 (stream_kernel)",
+            "kernel": "gate-up-SiLU bf16 M=1 (rows_kernel)",
             "bound": "hbm",
             "achieved": round(gu_gbs, 1),
             "peak": PEAK_HBM_GBS,
