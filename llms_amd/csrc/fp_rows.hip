@@ -3,19 +3,29 @@
 //
 // Each wave owns whole weight rows (gate-up: row n of Wg and row n of Wu) and
 // reads them front to back, one contiguous 1 KB run per wave instruction
-// (64 lanes x 16 B = 512 bf16 of one row), so each workgroup streams a
-// contiguous stretch of every matrix in address order — measured on MI355X
-// ~1 us per gate-up launch faster than gathering 128 B lines of eight rows.
-// With one x row the arithmetic is 2 flop per weight byte pair, so the dot
-// products run on the VALU (fp32 FMAs of unpacked bf16) and the MFMA pipe is
-// not used; lane l accumulates k = 512 j + 8 l .. +7 over the row's chunks j.
-// A row ends with a fixed-order wave reduction (DPP within 16-lane rows, then
-// the four row sums via readlane), the epilogue at the torch rounding points,
-// and one 2-byte store: no LDS reduction, no barrier after the prologue.
+// (64 lanes x 16 B: 512 bf16 or 1024 int8 of one row), so each workgroup
+// streams a contiguous stretch of every matrix in address order — measured on
+// MI355X ~1 us per gate-up launch faster than gathering 128 B lines of eight
+// rows. Lane l holds k = KC j + (KC/64) l .. of chunk j.
+// The dot products run on the matrix core with a diagonal trick: lane l
+// supplies the same k range to the A operand (its weights) and to the B
+// operand (its x), so D[i][i] of v_mfma_f32_16x16x32_bf16 is the partial dot
+// product of lanes i, i+16, i+32, i+48; the accumulator carries it over the
+// row's chunks and the off-diagonal entries are unused (with one x row the
+// matrix core has 16x the work it needs and is still ~7% busy). This takes
+// the per-element unpack and FMA off the VALU (measured: gate-up 18.3 vs
+// 19.1 us bf16, 13.8 vs 16.5 us int8).
+// int8 weights are dequantised in registers to bf16(q * s) exactly as the
+// dequantise-then-matmul path does (one fp32 rounding of q*s, then RNE to
+// bf16 with v_cvt_pk_bf16_f32).
+// A row ends with a fixed-order 64-lane sum of the diagonal (DPP within
+// 16-lane rows, then the four row sums via readlane), the epilogue at the
+// torch rounding points, and one 2-byte store: no LDS reduction, no barrier
+// after the prologue.
 // x (K bf16) is staged once per workgroup in LDS while the wave's first
 // weight loads are in flight.
-// Requirements (checked by rows_supported): M == 1, bf16, 16-byte-aligned
-// rows with K % 8 == 0, K <= kRowsMaxK.
+// Requirements (checked by rows_supported): M == 1, 16-byte-aligned rows with
+// K % 8 == 0 (int8: K % 16 == 0), K <= kRowsMaxK.
 #include "fp_common.h"
 #include "fp_launch.h"
 
@@ -23,7 +33,9 @@ namespace fp {
 
 namespace {
 
-constexpr int kKC = 512;  // k elements per wave instruction (64 lanes x 8)
+// k elements per wave instruction (64 lanes x 16 B)
+template <bool W8>
+constexpr int kc() { return W8 ? 1024 : 512; }
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -42,25 +54,46 @@ __device__ __forceinline__ float wave_sum(float v) {
           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48)));
 }
 
-// acc += sum over 8 bf16 pairs (w[e] * x[e]), in e order.
-__device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc) {
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xx[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    acc = fmaf(__uint_as_float(ww[d] << 16), __uint_as_float(xx[d] << 16), acc);
-    acc = fmaf(__uint_as_float(ww[d] & 0xffff0000u), __uint_as_float(xx[d] & 0xffff0000u), acc);
-  }
-  return acc;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+
+// Four int8 of one dword dequantised to bf16(q * s) and returned as two
+// packed bf16 pairs (bytes 0,1 and 2,3): fma(q + 128, s, -128 s) is the exact
+// product rounded once to fp32, the conversion is RNE.
+__device__ __forceinline__ u32x2 dequant4_bf16(uint32_t qword, float s, float n128s) {
+  const uint32_t u = qword ^ 0x80808080u;
+  const f32x2 lo = {fmaf((float)(u & 0xffu), s, n128s), fmaf((float)((u >> 8) & 0xffu), s, n128s)};
+  const f32x2 hi = {fmaf((float)((u >> 16) & 0xffu), s, n128s), fmaf((float)(u >> 24), s, n128s)};
+  return u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
+               __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2))};
+}
+
+// Eight int8 (two dwords) dequantised to eight packed bf16(q * s).
+__device__ __forceinline__ u32x4 dequant8_bf16(uint32_t q0, uint32_t q1, float s, float n128s) {
+  const u32x2 lo = dequant4_bf16(q0, s, n128s), hi = dequant4_bf16(q1, s, n128s);
+  return u32x4{lo.x, lo.y, hi.x, hi.y};
+}
+
+// Diagonal of a wave's 16x16 MFMA accumulator: lane l holds rows
+// 4 (l / 16) + r, column l % 16, so D[i][i] sits in lane 20 (i / 4) + i % 4,
+// register i % 4. Returns it there and 0 elsewhere.
+__device__ __forceinline__ float diag(f32x4 d, int lane) {
+  const int c = lane & 15;
+  if ((c >> 2) != (lane >> 4)) return 0.f;
+  const int r = c & 3;
+  return r == 0 ? d.x : r == 1 ? d.y : r == 2 ? d.z : d.w;
 }
 
 // NW waves per workgroup, R rows per wave, U weight chunks in flight per wave.
-template <int NW, int R, int U, bool GATEUP>
+template <int NW, int R, int U, bool GATEUP, bool W8>
 __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
+  constexpr int KC = kc<W8>();
+  constexpr int KL = KC / kWave;  // k elements per lane per chunk
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int64_t K = a.K;
-  const int J = (int)((K + kKC - 1) / kKC);  // chunks per row
+  const int J = (int)((K + KC - 1) / KC);  // chunks per row
   const int64_t row0 = ((int64_t)blockIdx.x * NW + wave) * R;
   const int64_t left = a.N - row0;
   const int nr = left <= 0 ? 0 : (left < R ? (int)left : R);
@@ -72,50 +105,82 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   auto issue = [&](int u) {
     if (ir < nr) {
       const int64_t row = row0 + ir;
-      const int64_t k = (int64_t)ij * kKC + 8 * lane;
-      wg[u] = load_bf16x8<true>((const uint16_t*)a.w0 + row * a.ldw0, k, K);
-      if constexpr (GATEUP) wu[u] = load_bf16x8<true>((const uint16_t*)a.w1 + row * a.ldw1, k, K);
+      const int64_t k = (int64_t)ij * KC + KL * lane;
+      if constexpr (W8) {
+        wg[u] = load_i8x16<true>((const int8_t*)a.w0 + row * a.ldw0, k, K);
+        if constexpr (GATEUP) wu[u] = load_i8x16<true>((const int8_t*)a.w1 + row * a.ldw1, k, K);
+      } else {
+        wg[u] = load_bf16x8<true>((const uint16_t*)a.w0 + row * a.ldw0, k, K);
+        if constexpr (GATEUP) wu[u] = load_bf16x8<true>((const uint16_t*)a.w1 + row * a.ldw1, k, K);
+      }
       if (++ij == J) { ij = 0; ++ir; }
     }
   };
 #pragma unroll
   for (int u = 0; u < U; ++u) issue(u);
 
-  // x[0:K] -> LDS, zero-padded to J * 512
-  const int64_t nvec = (int64_t)J * (kKC / 8);
+  // x[0:K] -> LDS, zero-padded to J * KC
+  const int64_t nvec = (int64_t)J * (KC / 8);
   for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave)
     *reinterpret_cast<u32x4*>(xs + i * 8) = load_bf16x8<true>(a.x, i * 8, K);
   __syncthreads();
 
-  float ag = 0.f, au = 0.f;
+  // int8 row scales of the row being consumed
+  float sg = 0.f, su = 0.f;
+  auto load_scales = [&](int r) {
+    if constexpr (W8) {
+      if (r < nr) {
+        sg = a.s0[row0 + r];
+        if constexpr (GATEUP) su = a.s1[row0 + r];
+      }
+    }
+  };
+  load_scales(0);
+
+  f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
   int cr = 0, cj = 0;  // (row, chunk) being consumed
   for (int t0 = 0; t0 < T; t0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (t0 + u < T) {
-        const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + (int64_t)cj * kKC + 8 * lane);
-        ag = dot8(wg[u], xv, ag);
-        if constexpr (GATEUP) au = dot8(wu[u], xv, au);
+        const uint16_t* xp = xs + (int64_t)cj * KC + KL * lane;
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(xp);
+        if constexpr (W8) {
+          const u32x4 xv1 = *reinterpret_cast<const u32x4*>(xp + 8);
+          const float ng = -128.f * sg;
+          dg = mfma16(dequant8_bf16(wg[u].x, wg[u].y, sg, ng), xv, dg);
+          dg = mfma16(dequant8_bf16(wg[u].z, wg[u].w, sg, ng), xv1, dg);
+          if constexpr (GATEUP) {
+            const float nu = -128.f * su;
+            du = mfma16(dequant8_bf16(wu[u].x, wu[u].y, su, nu), xv, du);
+            du = mfma16(dequant8_bf16(wu[u].z, wu[u].w, su, nu), xv1, du);
+          }
+        } else {
+          dg = mfma16(wg[u], xv, dg);
+          if constexpr (GATEUP) du = mfma16(wu[u], xv, du);
+        }
         issue(u);
         if (++cj == J) {
-          const float g = wave_sum(ag);
-          const float up = GATEUP ? wave_sum(au) : 0.f;
+          const float g = wave_sum(diag(dg, lane));
+          const float up = GATEUP ? wave_sum(diag(du, lane)) : 0.f;
+          dg = du = f32x4{0.f, 0.f, 0.f, 0.f};
           if (lane == 0)
             a.y[row0 + cr] = (uint16_t)(GATEUP ? gate_up_silu_bits(g, up) : f32_to_bf16_bits(g));
-          ag = au = 0.f;
           cj = 0;
           ++cr;
+          load_scales(cr);
         }
       }
     }
   }
 }
 
-template <int NW, int R, int U, bool GATEUP>
+template <int NW, int R, int U, bool GATEUP, bool W8>
 int launch_rows_cfg(const StreamArgs& a, hipStream_t s) {
+  constexpr int KC = kc<W8>();
   const int64_t per = (int64_t)NW * R;
-  const size_t shm = (size_t)((a.K + kKC - 1) / kKC) * kKC * 2;
-  hipLaunchKernelGGL((rows_kernel<NW, R, U, GATEUP>), dim3((unsigned)((a.N + per - 1) / per)),
+  const size_t shm = (size_t)((a.K + KC - 1) / KC) * KC * 2;
+  hipLaunchKernelGGL((rows_kernel<NW, R, U, GATEUP, W8>), dim3((unsigned)((a.N + per - 1) / per)),
                      dim3(NW * kWave), shm, s, a);
   return (int)hipGetLastError();
 }
@@ -126,16 +191,23 @@ bool rows_supported(const StreamArgs& a, bool aligned) {
   return aligned && a.M == 1 && a.K <= kRowsMaxK;
 }
 
-// Measured on MI355X (Qwen3-4B, 36 cycled weight sets): one row (pair) per
-// wave with its whole row in flight (K = 2560: 5 chunks); gate-up 4 waves per
-// workgroup, QKV 8.
-template <bool GATEUP>
+// Measured on MI355X (Qwen3-4B, 36 cycled weight sets): the whole row in
+// flight (K = 2560: 5 bf16 or 3 int8 chunks); bf16 one row (pair) per wave,
+// 8 waves per workgroup; int8 gate-up two row pairs per wave, 4 waves.
+template <bool GATEUP, bool W8>
 int launch_rows(const StreamArgs& a, hipStream_t s) {
-  if constexpr (GATEUP) return launch_rows_cfg<4, 1, 5, true>(a, s);
-  return launch_rows_cfg<8, 1, 5, false>(a, s);
+  if constexpr (W8) {
+    if constexpr (GATEUP) return launch_rows_cfg<4, 2, 3, true, true>(a, s);
+    return launch_rows_cfg<8, 1, 3, false, true>(a, s);
+  } else {
+    if constexpr (GATEUP) return launch_rows_cfg<8, 1, 5, true, false>(a, s);
+    return launch_rows_cfg<8, 1, 5, false, false>(a, s);
+  }
 }
 
-template int launch_rows<false>(const StreamArgs&, hipStream_t);
-template int launch_rows<true>(const StreamArgs&, hipStream_t);
+template int launch_rows<false, false>(const StreamArgs&, hipStream_t);
+template int launch_rows<true, false>(const StreamArgs&, hipStream_t);
+template int launch_rows<false, true>(const StreamArgs&, hipStream_t);
+template int launch_rows<true, true>(const StreamArgs&, hipStream_t);
 
 }  // namespace fp

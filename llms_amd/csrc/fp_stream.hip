@@ -350,8 +350,8 @@ int launch_stream_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // QKV 2 (QKV's 3x smaller grid is latency-bound and prefers occupancy).
 template <bool GATEUP, bool W8>
 int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
-  // a single bf16 row: contiguous row streaming (fp_rows.hip)
-  if (!W8 && rows_supported(a, aligned)) return launch_rows<GATEUP>(a, s);
+  // a single row: contiguous row streaming (fp_rows.hip)
+  if (rows_supported(a, aligned)) return launch_rows<GATEUP, W8>(a, s);
   // (int8 dequantisation needs registers of its own: 2 k-blocks per buffer)
   constexpr int U8 = (GATEUP && !W8) ? 4 : 2;
   if (a.M <= 8) return launch_stream_cfg<4, 1, U8, 0, GATEUP, W8, false, true>(a, aligned, s);

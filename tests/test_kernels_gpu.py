@@ -299,9 +299,29 @@ def test_qwen3_4b_int8(M):
     _check(y[rows], out, f"4B int8 gate-up M={M}")
 
 
+@pytest.mark.parametrize("M", [1, 4, 100])
+def test_int8_dequant_bit_exact(M):
+    """In-register dequantisation is bit-exact: with one-hot x rows the QKV
+    output is a single dequantised weight, y[m, n] = bf16(q[n, k_m] * s[n])
+    (a one-term sum is exact, then rounded to bf16, which it already is), so it
+    must equal the oracle's dequant_w8 column bit for bit — through the row
+    kernel (M = 1), the streaming kernel (M = 4) and the tiled one (M = 100)."""
+    K, N = 2560, 384
+    _, w = qkv_inputs(70 + M, 1, K, N - 128, 64, w_std=0.05)
+    q, s = _quant(w)
+    deq = ref.dequant_w8(q.cpu().numpy(), s.cpu().numpy())            # [N, K] bf16 bits
+    ks = np.random.default_rng(M).choice(K, size=M, replace=False)
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    x[np.arange(M), ks] = 1.0
+    yq, yk, yv = _kernels().fused_qkv_w8(x.to(DEV), q, s, n_q=N - 128, n_k=64)
+    y = bits(torch.cat([yq, yk, yv], -1).cpu())
+    np.testing.assert_array_equal(y, deq[:, ks].T)
+
+
 def test_int8_tails_and_zero_rows():
     kern = _kernels()
-    for M, K, N in [(3, 2541, 100), (70, 2541, 100), (5, 1040, 48), (90, 1040, 48)]:
+    for M, K, N in [(3, 2541, 100), (70, 2541, 100), (5, 1040, 48), (90, 1040, 48),
+                    (1, 16, 5), (1, 1040, 33), (1, 2541, 9), (1, 16384, 20), (1, 16400, 7)]:
         x, wg, wu = ffn_inputs(M + K, M, K, N)
         wg[3] = 0  # an all-zero row: s = 0, q = 0
         qg, sg = _quant(wg)
