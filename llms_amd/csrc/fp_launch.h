@@ -40,6 +40,15 @@ int launch_rows(const StreamArgs& a, hipStream_t s);
 template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s);
 
+// Split-K bf16 MFMA tiles for the middle regime (fp_splitk.hip): used by
+// launch_stream for kSplitkMinM <= M and by launch_tiled for small-N calls up
+// to kSplitkMaxM rows, when splitk_supported() holds.
+constexpr int64_t kSplitkMinM = 9;
+constexpr int64_t kSplitkMaxM = 256;
+bool splitk_supported(const StreamArgs& a, bool aligned);
+template <bool GATEUP>
+int launch_splitk(const StreamArgs& a, hipStream_t s);
+
 // Direct-to-LDS bf16 MFMA contraction (fp_gemm.hip), used by launch_tiled
 // when gemm_supported() holds.
 bool gemm_supported(const StreamArgs& a, bool aligned);

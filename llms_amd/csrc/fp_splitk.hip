@@ -1,0 +1,254 @@
+// fp_splitk.hip — fused projections for the middle regime (M from ~16 to a
+// few hundred rows): too many x rows for the weight-streaming kernels' register
+// budget, too few output tiles for the 256 x 256 prefill tiles to fill 256 CUs
+// (QKV has N = 6144: 24 tiles of 256 rows).
+//
+// A workgroup owns a small output tile: BN weight rows (gate-up: BN/2 rows of
+// Wg and BN/2 of Wu, interleaved in 16-row groups) x BM rows of x. Its NW
+// waves split K: wave w takes k-steps w, w + NW, w + 2 NW, ... (64 k each),
+// each wave with a private ring of NS LDS stages that it fills itself with
+// buffer_load_dwordx4 ... lds (8 tile rows x 128 B per instruction, whole
+// lines, XOR-swizzled so the fragment reads are conflict-free). The bytes in
+// flight therefore live in LDS, not in registers, and the main loop has no
+// barrier: a wave only waits for its own loads. After the last step the
+// waves' partial tiles are summed through LDS in fixed wave order and the
+// epilogue (bf16 store, or silu(g)*u at torch's rounding points) runs on
+// wave 0's share of the tile.
+// Requirements (checked by splitk_supported): bf16, K % 64 == 0,
+// 16-byte-aligned rows, operand byte sizes below 2^31.
+#include "fp_common.h"
+#include "fp_launch.h"
+
+namespace fp {
+
+namespace {
+
+constexpr int kBK = 64;                  // k per step
+constexpr int kCPR = kBK / 8;            // 16-byte chunks per tile row
+constexpr int kRPI = 1024 / (kBK * 2);   // tile rows per load instruction
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & (kCPR - 1); }
+
+// buffer_load_dwordx4 ... lds: 16 bytes per lane from base + voff + soff into
+// LDS at dst + 16 * lane; bytes at or past `nbytes` read as zero.
+__device__ __forceinline__ void load_lds16(const void* base, int nbytes, lds_ptr_t dst,
+                                           uint32_t voff, uint32_t soff) {
+  constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, kRsrcFlags), dst, 16,
+      voff, soff, 0, 0);
+}
+
+// s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= v only.
+constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >> 4) << 14); }
+
+template <int BN, int BM, int NW, int NS, bool GATEUP>
+__global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_mt) {
+  constexpr int FN = BN / 16, FM = BM / 16;  // MFMA sub-tiles (the whole tile per wave)
+  constexpr int IW = BN / kRPI, IX = BM / kRPI;  // load instructions per stage
+  constexpr int kPerStep = IW + IX;
+  static_assert(BN % 16 == 0 && BM % 16 == 0, "tile");
+  static_assert(!GATEUP || BN % 32 == 0, "gate-up tiles hold whole gate/up 16-row pairs");
+  static_assert(NS == 2 || NS == 3, "LDS stages");
+  // the partial tiles of waves 1 .. NW-1 are summed in stage 0's space
+  static_assert((NW - 1) * FN * FM * 256 * 4 <= NW * (BN + BM) * kBK * 2, "reduction space");
+
+  // One LDS object per stage (distinct alias scopes: reads of one stage are
+  // not ordered after the asynchronous writes into another), each split per
+  // wave into W rows then x rows.
+  __shared__ __attribute__((aligned(1024))) uint16_t sS0[NW][BN + BM][kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sS1[NW][BN + BM][kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sS2[NS > 2 ? NW : 1][BN + BM][kBK];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int li = lane & 15, grp = lane >> 4;
+
+  const int tm = blockIdx.x % n_mt, tn = blockIdx.x / n_mt;  // M-fastest: W tile reused in L2
+  const int64_t m0 = (int64_t)tm * BM;
+  const int64_t c0 = (int64_t)tn * (GATEUP ? BN / 2 : BN);  // first output column
+
+  // Per-lane byte offsets of this lane's 16 B in each load instruction (see
+  // fp_gemm.hip: instruction q fills tile rows 8q .. 8q+7, the swizzle is
+  // applied on the global side so the LDS writes stay lane-linear).
+  const int lrow = lane / kCPR, lchunk = lane % kCPR;
+  uint32_t woff[IW];
+#pragma unroll
+  for (int q = 0; q < IW; ++q) {
+    const int t = q * kRPI + lrow;
+    const int64_t n = GATEUP ? c0 + (t / 32) * 16 + (t % 16) : c0 + t;
+    const int64_t ld = (GATEUP && ((t / 16) & 1)) ? a.ldw1 : a.ldw0;
+    woff[q] = (uint32_t)(n * ld * 2) + (uint32_t)((lchunk ^ swz(t)) * 16);
+  }
+  uint32_t xoff[IX];
+#pragma unroll
+  for (int q = 0; q < IX; ++q) {
+    const int t = q * kRPI + lrow;
+    xoff[q] = (uint32_t)((m0 + t) * a.ldx * 2) + (uint32_t)((lchunk ^ swz(BN + t)) * 16);
+  }
+  const int wbytes0 = (int)((a.N - 1) * a.ldw0 * 2 + a.K * 2);
+  const int wbytes1 = GATEUP ? (int)((a.N - 1) * a.ldw1 * 2 + a.K * 2) : wbytes0;
+  const int xbytes = (int)((a.M - 1) * a.ldx * 2 + a.K * 2);
+  void* const wptr1 = (void*)(GATEUP ? a.w1 : a.w0);
+
+  auto stage = [&](int s) -> uint16_t (*)[kBK] {
+    return s == 0 ? sS0[wave] : (s == 1 ? sS1[wave] : sS2[NS > 2 ? wave : 0]);
+  };
+  auto issue = [&](int s, int64_t k0) {
+    uint16_t (*t)[kBK] = stage(s);
+    const uint32_t kb = (uint32_t)(k0 * 2);
+#pragma unroll
+    for (int q = 0; q < IW; ++q) {
+      const bool up = GATEUP && ((q / 2) & 1);  // 16-row groups alternate Wg, Wu
+      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0, (lds_ptr_t)&t[q * kRPI][0], woff[q], kb);
+    }
+#pragma unroll
+    for (int q = 0; q < IX; ++q)
+      load_lds16(a.x, xbytes, (lds_ptr_t)&t[BN + q * kRPI][0], xoff[q], kb);
+  };
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // fragment byte offsets (swz of row 16 i + li does not depend on i)
+  const uint32_t offa = (uint32_t)(li * kBK * 2 + ((grp ^ swz(li)) * 16));
+  const uint32_t offb = (uint32_t)((BN + li) * kBK * 2 + ((grp ^ swz(BN + li)) * 16));
+  auto compute = [&](int s) {
+    const char* t = (const char*)stage(s);
+#pragma unroll
+    for (int kk = 0; kk < kBK / 32; ++kk) {
+      const uint32_t oa = offa ^ (uint32_t)(kk * 64), ob = offb ^ (uint32_t)(kk * 64);
+      u32x4 fa[FN], fb[FM];
+#pragma unroll
+      for (int i = 0; i < FN; ++i) fa[i] = *reinterpret_cast<const u32x4*>(t + oa + i * 16 * kBK * 2);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) fb[j] = *reinterpret_cast<const u32x4*>(t + ob + j * 16 * kBK * 2);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
+    }
+  };
+
+  // This wave's k-steps: w, w + NW, ...; the ring keeps NS - 1 of them in
+  // flight while one is consumed.
+  const int64_t nkt = a.K / kBK;
+  const int64_t mine = nkt > wave ? (nkt - wave + NW - 1) / NW : 0;
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < mine) issue(s, (wave + (int64_t)NW * s) * kBK);
+  for (int64_t j0 = 0; j0 < mine; j0 += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int64_t j = j0 + u;
+      if (j >= mine) break;
+      if (j + NS - 1 < mine) {
+        issue((u + NS - 1) % NS, (wave + NW * (j + NS - 1)) * kBK);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 1) * kPerStep));
+      } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      }
+      compute(u);
+    }
+  }
+
+  // Fixed-order cross-wave sum through LDS (the ring is free now).
+  float* red = reinterpret_cast<float*>(&sS0[0][0][0]);
+  __syncthreads();
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        *reinterpret_cast<f32x4*>(red + (((wave - 1) * FN + i) * FM + j) * 256 + lane * 4) = acc[i][j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w = 0; w < NW - 1; ++w)
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        acc[i][j] += *reinterpret_cast<const f32x4*>(red + ((w * FN + i) * FM + j) * 256 + lane * 4);
+
+  // Epilogue: D lane holds rows 4*grp + r (weight rows) of column li (x row).
+  const bool y8 = ((a.ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 7) == 0);
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int64_t m = m0 + j * 16 + li;
+    if (m >= a.M) continue;
+    uint16_t* yrow = a.y + m * a.ldy;
+#pragma unroll
+    for (int i = 0; i < FN; i += (GATEUP ? 2 : 1)) {
+      int64_t nb;
+      uint32_t h[4];
+      if constexpr (GATEUP) {
+        nb = c0 + (i / 2) * 16 + 4 * grp;  // i even: gate group of pair i/2
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[r] = gate_up_silu_bits(acc[i][j][r], acc[i + 1][j][r]);
+      } else {
+        nb = c0 + i * 16 + 4 * grp;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16_bits(acc[i][j][r]);
+      }
+      if (y8 && nb + 3 < a.N) {
+        *reinterpret_cast<u32x2*>(yrow + nb) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nb + r < a.N) yrow[nb + r] = (uint16_t)h[r];
+      }
+    }
+  }
+}
+
+template <int BN, int BM, int NW, int NS, bool GATEUP>
+int launch_splitk_cfg(const StreamArgs& a, hipStream_t s) {
+  const int64_t cols = GATEUP ? BN / 2 : BN;
+  const int n_nt = (int)((a.N + cols - 1) / cols);
+  const int n_mt = (int)((a.M + BM - 1) / BM);
+  hipLaunchKernelGGL((splitk_kernel<BN, BM, NW, NS, GATEUP>), dim3((unsigned)(n_nt * n_mt)),
+                     dim3(NW * kWave), 0, s, a, n_mt);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+#ifndef FP_SPLITK_NO_DISPATCH
+bool splitk_supported(const StreamArgs& a, bool aligned) {
+  constexpr int64_t kLim = (int64_t)1 << 31;
+  if (!aligned || a.K % kBK != 0) return false;
+  if ((a.N - 1) * a.ldw0 * 2 + a.K * 2 >= kLim) return false;
+  if (a.w1 && (a.N - 1) * a.ldw1 * 2 + a.K * 2 >= kLim) return false;
+  if ((a.M - 1) * a.ldx * 2 + a.K * 2 >= kLim) return false;
+  return true;
+}
+
+// Tile table measured on MI355X (Qwen3-4B and -8B shapes, 12 cycled weight
+// sets): the x tile is M rounded up to 16 (up to 64 rows), then 64 x 64
+// tiles; gate-up tiles hold 16 outputs (32 weight rows).
+template <bool GATEUP>
+int launch_splitk(const StreamArgs& a, hipStream_t s) {
+  if constexpr (GATEUP) {
+    if (a.M <= 16) return launch_splitk_cfg<32, 16, 4, 3, true>(a, s);
+    if (a.M <= 32) return launch_splitk_cfg<32, 32, 8, 2, true>(a, s);
+    if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, true>(a, s);
+    return launch_splitk_cfg<64, 64, 4, 2, true>(a, s);
+  } else {
+    if (a.M <= 16) return launch_splitk_cfg<16, 16, 4, 3, false>(a, s);
+    if (a.M <= 32) return launch_splitk_cfg<32, 32, 4, 3, false>(a, s);
+    if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, false>(a, s);
+    return launch_splitk_cfg<64, 64, 4, 2, false>(a, s);
+  }
+}
+
+template int launch_splitk<false>(const StreamArgs&, hipStream_t);
+template int launch_splitk<true>(const StreamArgs&, hipStream_t);
+#endif
+
+}  // namespace fp

@@ -352,6 +352,8 @@ template <bool GATEUP, bool W8>
 int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
   // a single row: contiguous row streaming (fp_rows.hip)
   if (rows_supported(a, aligned)) return launch_rows<GATEUP, W8>(a, s);
+  // 9..64 bf16 rows: split-K tiles (fp_splitk.hip)
+  if (!W8 && a.M >= kSplitkMinM && splitk_supported(a, aligned)) return launch_splitk<GATEUP>(a, s);
   // (int8 dequantisation needs registers of its own: 2 k-blocks per buffer)
   constexpr int U8 = (GATEUP && !W8) ? 4 : 2;
   if (a.M <= 8) return launch_stream_cfg<4, 1, U8, 0, GATEUP, W8, false, true>(a, aligned, s);

@@ -255,6 +255,20 @@ def test_regime_boundaries(M):
     check_ffn(20 + M, M, 1024, 640)
 
 
+@pytest.mark.parametrize("M,K", [(9, 1024), (16, 64), (23, 320), (33, 2560), (48, 128),
+                                 (64, 4096), (65, 1024), (130, 2560), (256, 320)])
+def test_split_k_regime(M, K):
+    """9 <= M <= 64 (and QKV-sized N up to 256 rows) run the split-K tiles,
+    each wave of a workgroup with its own k-steps (64 k each, interleaved)
+    and a fixed-order reduction: a single k-step (waves without work), k-step
+    counts that do not divide evenly over the waves, x tiles of 16..64 rows
+    with ragged M, and N not a multiple of the 16/32-output tiles."""
+    check_qkv(80 + M, M, K, 256 + 48, 40, label=f"qkv M={M} K={K} N=384")
+    check_ffn(81 + M, M, K, 100, label=f"gate-up M={M} K={K} N=100")
+    if M <= 64:
+        check_ffn(82 + M, M, K, 1000, label=f"gate-up M={M} K={K} N=1000")
+
+
 @pytest.mark.parametrize("K,N", [(8, 5), (520, 33), (2536, 9701), (16384, 64), (16392, 24), (4096, 1)])
 def test_single_row_streaming_edges(K, N):
     """M = 1 bf16 runs the row-streaming kernel (one wave per weight row, K in
