@@ -28,10 +28,12 @@ struct StreamArgs {
 template <bool GATEUP, bool W8>
 int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s);
 
-// Row-streaming kernels for M == 1 (fp_rows.hip), bf16 and int8, used by
-// launch_stream when rows_supported() holds. x is staged in LDS:
-// K <= kRowsMaxK.
+// Row-streaming kernels for 1 <= M <= kRowsMaxM (fp_rows.hip), bf16 and
+// int8, used by launch_stream when rows_supported() holds. x is staged in
+// LDS: M * K <= kRowsMaxK.
+constexpr int64_t kRowsMaxM = 4;
 constexpr int64_t kRowsMaxK = 16384;
+template <bool W8>
 bool rows_supported(const StreamArgs& a, bool aligned);
 template <bool GATEUP, bool W8>
 int launch_rows(const StreamArgs& a, hipStream_t s);

@@ -1,5 +1,6 @@
-// fp_rows.hip — row-streaming fused projections for a single activation row
-// (M = 1, the decode step), where the call is one pass over the weights.
+// fp_rows.hip — row-streaming fused projections for one to four activation
+// rows (the decode step, short speculative verification), where the call is
+// one pass over the weights.
 //
 // Each wave owns whole weight rows (gate-up: row n of Wg and row n of Wu) and
 // reads them front to back, one contiguous 1 KB run per wave instruction
@@ -12,7 +13,8 @@
 // operand (its x), so D[i][i] of v_mfma_f32_16x16x32_bf16 is the partial dot
 // product of lanes i, i+16, i+32, i+48; the accumulator carries it over the
 // row's chunks and the off-diagonal entries are unused (with one x row the
-// matrix core has 16x the work it needs and is still ~7% busy). This takes
+// matrix core has 16x the work it needs and is still ~7% busy; each further
+// x row is one more MFMA per weight chunk with the same A operand). This takes
 // the per-element unpack and FMA off the VALU (measured: gate-up 18.3 vs
 // 19.1 us bf16, 13.8 vs 16.5 us int8).
 // int8 weights are dequantised in registers to bf16(q * s) exactly as the
@@ -22,10 +24,10 @@
 // 16-lane rows, then the four row sums via readlane), the epilogue at the
 // torch rounding points, and one 2-byte store: no LDS reduction, no barrier
 // after the prologue.
-// x (K bf16) is staged once per workgroup in LDS while the wave's first
-// weight loads are in flight.
-// Requirements (checked by rows_supported): M == 1, 16-byte-aligned rows with
-// K % 8 == 0 (int8: K % 16 == 0), K <= kRowsMaxK.
+// x (MM rows of K bf16, zero beyond M) is staged once per workgroup in LDS
+// while the wave's first weight loads are in flight.
+// Requirements (checked by rows_supported): M <= kRowsMaxM, 16-byte-aligned
+// rows with K % 8 == 0 (int8: K % 16 == 0), M * K <= kRowsMaxK.
 #include "fp_common.h"
 #include "fp_launch.h"
 
@@ -84,8 +86,9 @@ __device__ __forceinline__ float diag(f32x4 d, int lane) {
   return r == 0 ? d.x : r == 1 ? d.y : r == 2 ? d.z : d.w;
 }
 
-// NW waves per workgroup, R rows per wave, U weight chunks in flight per wave.
-template <int NW, int R, int U, bool GATEUP, bool W8>
+// NW waves per workgroup, R rows per wave, U weight chunks in flight per wave,
+// MM x rows (the call's M rounded up; the extra rows are zeros in LDS).
+template <int NW, int R, int U, int MM, bool GATEUP, bool W8>
 __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   constexpr int KC = kc<W8>();
   constexpr int KL = KC / kWave;  // k elements per lane per chunk
@@ -119,10 +122,14 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
 #pragma unroll
   for (int u = 0; u < U; ++u) issue(u);
 
-  // x[0:K] -> LDS, zero-padded to J * KC
-  const int64_t nvec = (int64_t)J * (KC / 8);
-  for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave)
-    *reinterpret_cast<u32x4*>(xs + i * 8) = load_bf16x8<true>(a.x, i * 8, K);
+  // x[0:MM, 0:K] -> LDS rows of Kp = J * KC, zero beyond K and beyond M
+  const int64_t Kp = (int64_t)J * KC;
+  const int64_t nvec = MM * (Kp / 8);
+  for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave) {
+    const int64_t m = i / (Kp / 8), k = (i - m * (Kp / 8)) * 8;
+    *reinterpret_cast<u32x4*>(xs + i * 8) =
+        m < a.M ? load_bf16x8<true>(a.x + m * a.ldx, k, K) : u32x4{0, 0, 0, 0};
+  }
   __syncthreads();
 
   // int8 row scales of the row being consumed
@@ -137,35 +144,55 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   };
   load_scales(0);
 
-  f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = {0.f, 0.f, 0.f, 0.f};
+  f32x4 dg[MM], du[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) dg[m] = du[m] = f32x4{0.f, 0.f, 0.f, 0.f};
   int cr = 0, cj = 0;  // (row, chunk) being consumed
   for (int t0 = 0; t0 < T; t0 += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (t0 + u < T) {
         const uint16_t* xp = xs + (int64_t)cj * KC + KL * lane;
-        const u32x4 xv = *reinterpret_cast<const u32x4*>(xp);
         if constexpr (W8) {
-          const u32x4 xv1 = *reinterpret_cast<const u32x4*>(xp + 8);
           const float ng = -128.f * sg;
-          dg = mfma16(dequant8_bf16(wg[u].x, wg[u].y, sg, ng), xv, dg);
-          dg = mfma16(dequant8_bf16(wg[u].z, wg[u].w, sg, ng), xv1, dg);
+          const u32x4 g0 = dequant8_bf16(wg[u].x, wg[u].y, sg, ng);
+          const u32x4 g1 = dequant8_bf16(wg[u].z, wg[u].w, sg, ng);
+          u32x4 u0, u1;
           if constexpr (GATEUP) {
             const float nu = -128.f * su;
-            du = mfma16(dequant8_bf16(wu[u].x, wu[u].y, su, nu), xv, du);
-            du = mfma16(dequant8_bf16(wu[u].z, wu[u].w, su, nu), xv1, du);
+            u0 = dequant8_bf16(wu[u].x, wu[u].y, su, nu);
+            u1 = dequant8_bf16(wu[u].z, wu[u].w, su, nu);
+          }
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(xp + m * Kp);
+            const u32x4 xv1 = *reinterpret_cast<const u32x4*>(xp + m * Kp + 8);
+            dg[m] = mfma16(g0, xv, dg[m]);
+            dg[m] = mfma16(g1, xv1, dg[m]);
+            if constexpr (GATEUP) {
+              du[m] = mfma16(u0, xv, du[m]);
+              du[m] = mfma16(u1, xv1, du[m]);
+            }
           }
         } else {
-          dg = mfma16(wg[u], xv, dg);
-          if constexpr (GATEUP) du = mfma16(wu[u], xv, du);
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(xp + m * Kp);
+            dg[m] = mfma16(wg[u], xv, dg[m]);
+            if constexpr (GATEUP) du[m] = mfma16(wu[u], xv, du[m]);
+          }
         }
         issue(u);
         if (++cj == J) {
-          const float g = wave_sum(diag(dg, lane));
-          const float up = GATEUP ? wave_sum(diag(du, lane)) : 0.f;
-          dg = du = f32x4{0.f, 0.f, 0.f, 0.f};
-          if (lane == 0)
-            a.y[row0 + cr] = (uint16_t)(GATEUP ? gate_up_silu_bits(g, up) : f32_to_bf16_bits(g));
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            const float g = wave_sum(diag(dg[m], lane));
+            const float up = GATEUP ? wave_sum(diag(du[m], lane)) : 0.f;
+            dg[m] = du[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (lane == 0 && m < a.M)
+              a.y[m * a.ldy + row0 + cr] =
+                  (uint16_t)(GATEUP ? gate_up_silu_bits(g, up) : f32_to_bf16_bits(g));
+          }
           cj = 0;
           ++cr;
           load_scales(cr);
@@ -175,34 +202,51 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   }
 }
 
-template <int NW, int R, int U, bool GATEUP, bool W8>
+template <int NW, int R, int U, int MM, bool GATEUP, bool W8>
 int launch_rows_cfg(const StreamArgs& a, hipStream_t s) {
   constexpr int KC = kc<W8>();
   const int64_t per = (int64_t)NW * R;
-  const size_t shm = (size_t)((a.K + KC - 1) / KC) * KC * 2;
-  hipLaunchKernelGGL((rows_kernel<NW, R, U, GATEUP, W8>), dim3((unsigned)((a.N + per - 1) / per)),
+  const size_t shm = (size_t)MM * ((a.K + KC - 1) / KC) * KC * 2;
+  hipLaunchKernelGGL((rows_kernel<NW, R, U, MM, GATEUP, W8>), dim3((unsigned)((a.N + per - 1) / per)),
                      dim3(NW * kWave), shm, s, a);
   return (int)hipGetLastError();
 }
 
 }  // namespace
 
+// bf16 takes M <= 2 here (for 3..4 rows the 8-row streaming kernel is
+// faster: its MFMA columns hold the x rows), int8 up to kRowsMaxM (the
+// dequantisation, shared by all x rows, dominates).
+template <bool W8>
 bool rows_supported(const StreamArgs& a, bool aligned) {
-  return aligned && a.M == 1 && a.K <= kRowsMaxK;
+  const int64_t max_m = W8 ? kRowsMaxM : 2;
+  return aligned && a.M >= 1 && a.M <= max_m && a.M * a.K <= kRowsMaxK;
 }
 
-// Measured on MI355X (Qwen3-4B, 36 cycled weight sets): the whole row in
-// flight (K = 2560: 5 bf16 or 3 int8 chunks); bf16 one row (pair) per wave,
-// 8 waves per workgroup; int8 gate-up two row pairs per wave, 4 waves.
+template bool rows_supported<false>(const StreamArgs&, bool);
+template bool rows_supported<true>(const StreamArgs&, bool);
+
+// Measured on MI355X (Qwen3-4B and -8B, 24-36 cycled weight sets): the whole
+// row in flight (K = 2560: 5 bf16 or 3 int8 chunks); bf16 one row (pair) per
+// wave, 8 waves per workgroup; int8 gate-up two row pairs per wave and 4
+// waves up to 2 x rows, one and 8 waves for 3..4; x rows rounded up to 1, 2, 4.
+template <int MM, bool GATEUP, bool W8>
+int launch_rows_m(const StreamArgs& a, hipStream_t s) {
+  if constexpr (W8) {
+    if constexpr (GATEUP && MM <= 2) return launch_rows_cfg<4, 2, 3, MM, true, true>(a, s);
+    if constexpr (GATEUP) return launch_rows_cfg<8, 1, 3, MM, true, true>(a, s);
+    return launch_rows_cfg<8, 1, 3, MM, false, true>(a, s);
+  } else {
+    if constexpr (GATEUP) return launch_rows_cfg<8, 1, 5, MM, true, false>(a, s);
+    return launch_rows_cfg<8, 1, 5, MM, false, false>(a, s);
+  }
+}
+
 template <bool GATEUP, bool W8>
 int launch_rows(const StreamArgs& a, hipStream_t s) {
-  if constexpr (W8) {
-    if constexpr (GATEUP) return launch_rows_cfg<4, 2, 3, true, true>(a, s);
-    return launch_rows_cfg<8, 1, 3, false, true>(a, s);
-  } else {
-    if constexpr (GATEUP) return launch_rows_cfg<8, 1, 5, true, false>(a, s);
-    return launch_rows_cfg<8, 1, 5, false, false>(a, s);
-  }
+  if (a.M == 1) return launch_rows_m<1, GATEUP, W8>(a, s);
+  if (a.M == 2) return launch_rows_m<2, GATEUP, W8>(a, s);
+  return launch_rows_m<4, GATEUP, W8>(a, s);
 }
 
 template int launch_rows<false, false>(const StreamArgs&, hipStream_t);

@@ -350,8 +350,8 @@ int launch_stream_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // QKV 2 (QKV's 3x smaller grid is latency-bound and prefers occupancy).
 template <bool GATEUP, bool W8>
 int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
-  // a single row: contiguous row streaming (fp_rows.hip)
-  if (rows_supported(a, aligned)) return launch_rows<GATEUP, W8>(a, s);
+  // one or a few rows: contiguous row streaming (fp_rows.hip)
+  if (rows_supported<W8>(a, aligned)) return launch_rows<GATEUP, W8>(a, s);
   // 9..64 bf16 rows: split-K tiles (fp_splitk.hip)
   if (!W8 && a.M >= kSplitkMinM && splitk_supported(a, aligned)) return launch_splitk<GATEUP>(a, s);
   // (int8 dequantisation needs registers of its own: 2 k-blocks per buffer)

@@ -269,16 +269,19 @@ def test_split_k_regime(M, K):
         check_ffn(82 + M, M, K, 1000, label=f"gate-up M={M} K={K} N=1000")
 
 
-@pytest.mark.parametrize("K,N", [(8, 5), (520, 33), (2536, 9701), (16384, 64), (16392, 24), (4096, 1)])
-def test_single_row_streaming_edges(K, N):
-    """M = 1 bf16 runs the row-streaming kernel (one wave per weight row, K in
-    512-element chunks, x in LDS up to K = 16384): tiny and ragged K (the last
-    chunk partly past the row), N not a multiple of the rows per workgroup,
-    the largest K it takes and the first K it hands to the streaming kernel."""
+@pytest.mark.parametrize("M,K,N", [(1, 8, 5), (1, 520, 33), (1, 2536, 9701), (1, 16384, 64),
+                                   (1, 16392, 24), (1, 4096, 1), (2, 8, 7), (2, 2536, 1001),
+                                   (2, 8192, 40), (2, 8200, 24)])
+def test_row_streaming_edges(M, K, N):
+    """M <= 2 bf16 runs the row-streaming kernel (one wave per weight row, K
+    in 512-element chunks, M x rows in LDS up to M * K = 16384): tiny and
+    ragged K (the last chunk partly past the row), N not a multiple of the
+    rows per workgroup, the largest K it takes and the first K it hands to
+    the streaming kernel."""
     n_q = max(N - 2 * (N // 4), 1)
     n_k = (N - n_q) // 2
-    check_qkv(40 + K, 1, K, n_q, n_k, label=f"qkv M=1 K={K} N={n_q + 2 * n_k}")
-    check_ffn(41 + K, 1, K, N, label=f"gate-up M=1 K={K} N={N}")
+    check_qkv(40 + K + M, M, K, n_q, n_k, label=f"qkv M={M} K={K} N={n_q + 2 * n_k}")
+    check_ffn(41 + K + M, M, K, N, label=f"gate-up M={M} K={K} N={N}")
 
 
 # ----- int8 weight-only --------------------------------------------------------
@@ -335,7 +338,8 @@ def test_int8_dequant_bit_exact(M):
 def test_int8_tails_and_zero_rows():
     kern = _kernels()
     for M, K, N in [(3, 2541, 100), (70, 2541, 100), (5, 1040, 48), (90, 1040, 48),
-                    (1, 16, 5), (1, 1040, 33), (1, 2541, 9), (1, 16384, 20), (1, 16400, 7)]:
+                    (1, 16, 5), (1, 1040, 33), (1, 2541, 9), (1, 16384, 20), (1, 16400, 7),
+                    (2, 1040, 33), (3, 2560, 17), (4, 4096, 9), (4, 4112, 5)]:
         x, wg, wu = ffn_inputs(M + K, M, K, N)
         wg[3] = 0  # an all-zero row: s = 0, q = 0
         qg, sg = _quant(wg)
