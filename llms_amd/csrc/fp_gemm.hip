@@ -253,13 +253,24 @@ bool gemm_supported(const StreamArgs& a, bool aligned) {
   return true;
 }
 
-// Tile table for the bf16 prefill path (measured on MI355X, Qwen3-4B
-// shapes): 8 waves; above M = 1024 tiles of 256 weight rows x 256 x rows
-// (64 x 128 per wave), below that 128 x 256 (64 x 64 per wave) so that small
-// calls still spread over more workgroups.
+// Tile table for the bf16 prefill path, measured on MI355X with Qwen3-4B and
+// -8B shapes. What decides is how many rounds of workgroups a call needs on
+// 256 CUs: 256 x 256 tiles (1 workgroup per CU) run best once they fill the
+// chip, smaller tiles (2 per CU) win where they save a round. QKV-sized
+// outputs (<= 8192 weight rows): 64 x 128 tiles with three stages to 768 rows,
+// 128 x 128 to 1536, then 256 x 256. Gate-up-sized: 128 x 128 to 384 rows,
+// 256 x 256 to 768 (152-192 tiles, one round), 128 x 128 to 1536, 256 x 256.
 template <bool GATEUP>
 int launch_gemm(const StreamArgs& a, hipStream_t s) {
-  if (a.M <= 1024) return launch_gemm_cfg<128, 256, 2, 4, GATEUP, 2>(a, s);
+  const int64_t wrows = GATEUP ? 2 * a.N : a.N;
+  if (wrows <= 8192) {
+    if (a.M <= 768) return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
+    if (a.M <= 1536) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
+    return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
+  }
+  if (a.M <= 384) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
+  if (a.M <= 768) return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
+  if (a.M <= 1536) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
   return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
 }
 
