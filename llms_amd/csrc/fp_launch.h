@@ -43,9 +43,12 @@ template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s);
 
 // Split-K bf16 MFMA tiles for the middle regime (fp_splitk.hip): used by
-// launch_stream for kSplitkMinM <= M and by launch_tiled for small-N calls up
-// to kSplitkMaxM rows, when splitk_supported() holds.
-constexpr int64_t kSplitkMinM = 9;
+// launch_stream from kSplitkMinM rows (kSplitkMinMSmallN for calls with at
+// most kSplitkSmallN weight rows) and by launch_tiled for small-N calls up to
+// kSplitkMaxM rows, when splitk_supported() holds.
+constexpr int64_t kSplitkMinM = 8;
+constexpr int64_t kSplitkMinMSmallN = 3;
+constexpr int64_t kSplitkSmallN = 8192;
 constexpr int64_t kSplitkMaxM = 256;
 bool splitk_supported(const StreamArgs& a, bool aligned);
 template <bool GATEUP>

@@ -1,5 +1,5 @@
-// fp_splitk.hip — fused projections for the middle regime (M from ~16 to a
-// few hundred rows): too many x rows for the weight-streaming kernels' register
+// fp_splitk.hip — fused projections for the middle regime (from 3-8 rows up to
+// a few hundred): too many x rows for the weight-streaming kernels' register
 // budget, too few output tiles for the 256 x 256 prefill tiles to fill 256 CUs
 // (QKV has N = 6144: 24 tiles of 256 rows).
 //

@@ -352,8 +352,10 @@ template <bool GATEUP, bool W8>
 int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
   // one or a few rows: contiguous row streaming (fp_rows.hip)
   if (rows_supported<W8>(a, aligned)) return launch_rows<GATEUP, W8>(a, s);
-  // 9..64 bf16 rows: split-K tiles (fp_splitk.hip)
-  if (!W8 && a.M >= kSplitkMinM && splitk_supported(a, aligned)) return launch_splitk<GATEUP>(a, s);
+  // bf16 from 3 (small N, e.g. QKV) or 8 rows: split-K tiles (fp_splitk.hip)
+  const int64_t wrows = GATEUP ? 2 * a.N : a.N;
+  const int64_t min_m = wrows <= kSplitkSmallN ? kSplitkMinMSmallN : kSplitkMinM;
+  if (!W8 && a.M >= min_m && splitk_supported(a, aligned)) return launch_splitk<GATEUP>(a, s);
   // (int8 dequantisation needs registers of its own: 2 k-blocks per buffer)
   constexpr int U8 = (GATEUP && !W8) ? 4 : 2;
   if (a.M <= 8) return launch_stream_cfg<4, 1, U8, 0, GATEUP, W8, false, true>(a, aligned, s);

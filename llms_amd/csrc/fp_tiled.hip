@@ -214,7 +214,7 @@ int launch_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
-  if (!W8 && a.M <= kSplitkMaxM && wrows <= 8192 && splitk_supported(a, aligned))
+  if (!W8 && a.M <= kSplitkMaxM && wrows <= kSplitkSmallN && splitk_supported(a, aligned))
     return launch_splitk<GATEUP>(a, s);
   if (!W8 && gemm_supported(a, aligned)) return launch_gemm<GATEUP>(a, s);
   return launch_cfg<128, 128, 64, 2, 2, GATEUP, W8>(a, aligned, s);
