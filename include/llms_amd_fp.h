@@ -106,6 +106,27 @@ int fp_gate_up_silu_w8(const void* x, int64_t ldx,
                        void* stream);
 
 /*
+ * Plain projection y = x W^T (bf16 out, no split, no epilogue): the MLP
+ * `down` and the attention `o` projections next to the fused path. Replaces
+ * the eager nn.Linear calls self.down(...) (reference: src/engine/model.py:37)
+ * and self.o(...) (reference: src/engine/attention.py:98, :183). Runs the same
+ * kernels as fp_qkv_bf16 (which it equals for n_q = N, n_k = 0).
+ *   x [M, K] bf16, w [N, K] bf16, y [M, N] bf16.  M >= 0, N >= 1, K >= 1.
+ */
+int fp_linear_bf16(const void* x, int64_t ldx,
+                   const void* w, int64_t ldw,
+                   void* y, int64_t ldy,
+                   int64_t M, int64_t N, int64_t K,
+                   void* stream);
+
+/* int8 weight-only plain projection (no reference counterpart, as above). */
+int fp_linear_w8(const void* x, int64_t ldx,
+                 const int8_t* q, int64_t ldq, const float* scale,
+                 void* y, int64_t ldy,
+                 int64_t M, int64_t N, int64_t K,
+                 void* stream);
+
+/*
  * Per-output-channel symmetric int8 quantisation on the device (the packing
  * step run once at swap time; no reference counterpart).
  *   s[r] = max_k |w[r,k]| / 127   (fp32; rows that are all zero get s = 0)

@@ -36,6 +36,8 @@ CAPI_SIGNATURES: dict[str, list] = {
     "fp_gate_up_silu_bf16": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "fp_qkv_w8": [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],
     "fp_gate_up_silu_w8": [_P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "fp_linear_bf16": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
+    "fp_linear_w8": [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P],
     "fp_quantize_w8_per_row": [_P, _I64, _P, _I64, _P, _I64, _I64, _P],
 }
 

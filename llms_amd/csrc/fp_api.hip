@@ -79,7 +79,7 @@ const char* fp_status_string(int status) {
   }
 }
 
-int fp_abi_version(void) { return (1 << 16) | 0; }
+int fp_abi_version(void) { return (1 << 16) | 1; }
 
 int fp_qkv_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
                 int64_t M, int64_t n_q, int64_t n_k, int64_t K, void* stream) {
@@ -142,6 +142,16 @@ int fp_gate_up_silu_w8(const void* x, int64_t ldx, const int8_t* qg, int64_t ldq
   const bool aligned = (K % 16 == 0) && (ldx % 8 == 0) && (ldqg % 16 == 0) &&
                        (ldqu % 16 == 0) && fp::al16(x) && fp::al16(qg) && fp::al16(qu);
   return fp::run<true, true>(a, aligned, (hipStream_t)stream);
+}
+
+int fp_linear_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                   int64_t M, int64_t N, int64_t K, void* stream) {
+  return fp_qkv_bf16(x, ldx, w, ldw, y, ldy, M, N, 0, K, stream);
+}
+
+int fp_linear_w8(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,
+                 void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
+  return fp_qkv_w8(x, ldx, q, ldq, scale, y, ldy, M, N, 0, K, stream);
 }
 
 int fp_quantize_w8_per_row(const void* w, int64_t ldw, int8_t* q, int64_t ldq, float* scale,

@@ -258,11 +258,19 @@ bool gemm_supported(const StreamArgs& a, bool aligned) {
 // 256 CUs: 256 x 256 tiles (1 workgroup per CU) run best once they fill the
 // chip, smaller tiles (2 per CU) win where they save a round. QKV-sized
 // outputs (<= 8192 weight rows): 64 x 128 tiles with three stages to 768 rows,
-// 128 x 128 to 1536, then 256 x 256. Gate-up-sized: 128 x 128 to 384 rows,
-// 256 x 256 to 768 (152-192 tiles, one round), 128 x 128 to 1536, 256 x 256.
+// 128 x 128 to 1536, then 256 x 256. Outputs of at most 4096 columns (the
+// down and o projections) keep 128 x 128 to 4096 rows: a 256 x 256 grid
+// there is under one round (2048 x 2560 -> 80 tiles). Gate-up-sized: 128 x
+// 128 to 384 rows, 256 x 256 to 768 (152-192 tiles, one round), 128 x 128 to
+// 1536, 256 x 256.
 template <bool GATEUP>
 int launch_gemm(const StreamArgs& a, hipStream_t s) {
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
+  if (wrows <= 4096) {
+    if (a.M <= 768) return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
+    if (a.M <= 4096) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
+    return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
+  }
   if (wrows <= 8192) {
     if (a.M <= 768) return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
     if (a.M <= 1536) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);

@@ -30,9 +30,10 @@ int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s);
 
 // Row-streaming kernels for 1 <= M <= kRowsMaxM (fp_rows.hip), bf16 and
 // int8, used by launch_stream when rows_supported() holds. x is staged in
-// LDS: M * K <= kRowsMaxK.
+// LDS (M rounded up to 1, 2 or 4 rows, K to whole chunks): at most
+// kRowsMaxLds bytes.
 constexpr int64_t kRowsMaxM = 4;
-constexpr int64_t kRowsMaxK = 16384;
+constexpr int64_t kRowsMaxLds = 65536;
 template <bool W8>
 bool rows_supported(const StreamArgs& a, bool aligned);
 template <bool GATEUP, bool W8>

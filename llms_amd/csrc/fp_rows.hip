@@ -27,7 +27,7 @@
 // x (MM rows of K bf16, zero beyond M) is staged once per workgroup in LDS
 // while the wave's first weight loads are in flight.
 // Requirements (checked by rows_supported): M <= kRowsMaxM, 16-byte-aligned
-// rows with K % 8 == 0 (int8: K % 16 == 0), M * K <= kRowsMaxK.
+// rows with K % 8 == 0 (int8: K % 16 == 0), staged x within kRowsMaxLds.
 #include "fp_common.h"
 #include "fp_launch.h"
 
@@ -202,11 +202,20 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   }
 }
 
+// x rows staged per workgroup: M rounded up to 1, 2 or 4
+inline int64_t rows_mm(int64_t M) { return M <= 2 ? M : 4; }
+
+// LDS bytes of the staged x: MM rows of K rounded up to whole chunks
+template <bool W8>
+int64_t rows_lds_bytes(int64_t M, int64_t K) {
+  constexpr int KC = kc<W8>();
+  return rows_mm(M) * ((K + KC - 1) / KC) * KC * 2;
+}
+
 template <int NW, int R, int U, int MM, bool GATEUP, bool W8>
 int launch_rows_cfg(const StreamArgs& a, hipStream_t s) {
-  constexpr int KC = kc<W8>();
   const int64_t per = (int64_t)NW * R;
-  const size_t shm = (size_t)MM * ((a.K + KC - 1) / KC) * KC * 2;
+  const size_t shm = (size_t)rows_lds_bytes<W8>(MM, a.K);
   hipLaunchKernelGGL((rows_kernel<NW, R, U, MM, GATEUP, W8>), dim3((unsigned)((a.N + per - 1) / per)),
                      dim3(NW * kWave), shm, s, a);
   return (int)hipGetLastError();
@@ -220,7 +229,7 @@ int launch_rows_cfg(const StreamArgs& a, hipStream_t s) {
 template <bool W8>
 bool rows_supported(const StreamArgs& a, bool aligned) {
   const int64_t max_m = W8 ? kRowsMaxM : 2;
-  return aligned && a.M >= 1 && a.M <= max_m && a.M * a.K <= kRowsMaxK;
+  return aligned && a.M >= 1 && a.M <= max_m && rows_lds_bytes<W8>(a.M, a.K) <= kRowsMaxLds;
 }
 
 template bool rows_supported<false>(const StreamArgs&, bool);

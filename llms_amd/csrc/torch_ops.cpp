@@ -92,6 +92,34 @@ at::Tensor gate_up_silu_w8(const at::Tensor& x, const at::Tensor& qg, const at::
   return y;
 }
 
+at::Tensor linear(const at::Tensor& x, const at::Tensor& w) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(w, "W", at::kBFloat16);
+  const c10::DeviceGuard guard(x.device());
+  const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
+  at::Tensor y = at::empty({M, N}, x.options());
+  check_status(fp_linear_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
+                              y.stride(0), M, N, K, cur_stream(x)),
+               "fp_linear_bf16");
+  return y;
+}
+
+at::Tensor linear_w8(const at::Tensor& x, const at::Tensor& q, const at::Tensor& s) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(q, "q", at::kChar);
+  TORCH_CHECK(s.dim() == 1 && s.scalar_type() == at::kFloat && s.is_contiguous(),
+              "scale must be a contiguous 1-D float32 tensor");
+  TORCH_CHECK(s.size(0) == q.size(0), "scale has ", s.size(0), " rows, q has ", q.size(0));
+  const c10::DeviceGuard guard(x.device());
+  const int64_t M = x.size(0), K = x.size(1), N = q.size(0);
+  at::Tensor y = at::empty({M, N}, x.options());
+  check_status(fp_linear_w8(x.data_ptr(), x.stride(0), (const int8_t*)q.data_ptr(), q.stride(0),
+                            s.data_ptr<float>(), y.data_ptr(), y.stride(0), M, N, K,
+                            cur_stream(x)),
+               "fp_linear_w8");
+  return y;
+}
+
 std::tuple<at::Tensor, at::Tensor> quantize_w8(const at::Tensor& w) {
   check_2d(w, "W", at::kBFloat16);
   const c10::DeviceGuard guard(w.device());
@@ -111,6 +139,8 @@ TORCH_LIBRARY(llms_amd, m) {
   m.def("gate_up_silu(Tensor x, Tensor wg, Tensor wu) -> Tensor");
   m.def("qkv_w8(Tensor x, Tensor q, Tensor scale, int n_q, int n_k) -> Tensor");
   m.def("gate_up_silu_w8(Tensor x, Tensor qg, Tensor sg, Tensor qu, Tensor su) -> Tensor");
+  m.def("linear(Tensor x, Tensor w) -> Tensor");
+  m.def("linear_w8(Tensor x, Tensor q, Tensor scale) -> Tensor");
   m.def("quantize_w8(Tensor w) -> (Tensor, Tensor)");
 }
 
@@ -119,5 +149,7 @@ TORCH_LIBRARY_IMPL(llms_amd, CUDA, m) {
   m.impl("gate_up_silu", gate_up_silu);
   m.impl("qkv_w8", qkv_w8);
   m.impl("gate_up_silu_w8", gate_up_silu_w8);
+  m.impl("linear", linear);
+  m.impl("linear_w8", linear_w8);
   m.impl("quantize_w8", quantize_w8);
 }

@@ -10,11 +10,14 @@ keyword arguments and semantics):
 
 from __future__ import annotations
 
+import itertools
+
 import torch
 from torch import nn
 
 from .fused_ffn import TritonFFN
 from .fused_qkv import TritonAttention
+from .linear import FusedLinear
 
 
 def apply_triton_kernels(
@@ -23,19 +26,36 @@ def apply_triton_kernels(
     fused_ffn: bool = True,
     fused_qkv: bool = True,
     int8: bool = False,
+    linear_down_o: bool = False,
 ) -> nn.Module:
     """Replace ``block.ffn`` / ``block.attn`` of every ``model.layers`` block
     with ``TritonFFN`` / ``TritonAttention`` (reference ``swap.py:22-46``).
 
     Idempotent: blocks already swapped are left as they are. ``int8=True``
     (not in the reference) builds the int8 weight-only modules instead.
+    ``linear_down_o=True`` (not in the reference) also replaces each block's
+    ``ffn.down`` and ``attn.o`` Linears with :class:`FusedLinear`, int8 when
+    ``int8`` is set.
     """
     for block in model.layers:
         if fused_ffn and not isinstance(block.ffn, TritonFFN):
             block.ffn = TritonFFN.from_eager(block.ffn, int8=int8)
         if fused_qkv and not isinstance(block.attn, TritonAttention):
             block.attn = TritonAttention.from_eager(block.attn, int8=int8)
+        if linear_down_o:
+            if not isinstance(block.ffn.down, FusedLinear):
+                block.ffn.down = FusedLinear.from_linear(block.ffn.down, int8=int8)
+            if not isinstance(block.attn.o, FusedLinear):
+                block.attn.o = FusedLinear.from_linear(block.attn.o, int8=int8)
     return model
+
+
+def _device(module: nn.Module) -> torch.device:
+    """The device of a module's first parameter or buffer (int8 modules keep
+    their weights as buffers)."""
+    for t in itertools.chain(module.parameters(), module.buffers()):
+        return t.device
+    raise ValueError(f"{type(module).__name__} holds no tensors")
 
 
 def prewarm_triton_kernels(
@@ -61,18 +81,27 @@ def prewarm_triton_kernels(
         if isinstance(m, TritonAttention):
             w = m.q_qkv if m.int8 else m.W_qkv
             attn_by_shape.setdefault((m.int8, *w.shape), m)
-    if not ffn_by_shape and not attn_by_shape:
+    lin_by_shape: dict[tuple, FusedLinear] = {}
+    for m in model.modules():
+        if isinstance(m, FusedLinear):
+            w = m.q if m.int8 else m.weight
+            lin_by_shape.setdefault((m.int8, *w.shape), m)
+    if not ffn_by_shape and not attn_by_shape and not lin_by_shape:
         return
 
     with torch.inference_mode():
         for (_, _, K), ffn in ffn_by_shape.items():
-            dev = ffn.down.weight.device
+            dev = _device(ffn)
             for M in m_values:
                 ffn.gate_up(torch.zeros((1, M, K), dtype=torch.bfloat16, device=dev))
         for (_, _, K), attn in attn_by_shape.items():
-            dev = attn.o.weight.device
+            dev = _device(attn)
             for M in m_values:
                 attn.project(torch.zeros((1, M, K), dtype=torch.bfloat16, device=dev))
+        for (_, _, K), lin in lin_by_shape.items():
+            dev = _device(lin)
+            for M in m_values:
+                lin(torch.zeros((1, M, K), dtype=torch.bfloat16, device=dev))
 
     if torch.cuda.is_available():
         torch.cuda.synchronize()

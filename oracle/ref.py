@@ -15,6 +15,8 @@ those of the torch path the reference runs when the fused kernels are off:
   ``tests/test_kernels_fused_ffn.py:21-30``): ``g = bf16(x.Wg^T)``,
   ``u = bf16(x.Wu^T)``, ``s = bf16(silu(g))`` with silu evaluated on the
   rounded g, ``y = bf16(s * u)``.
+- plain projections ``down`` / ``o`` (``src/engine/model.py:37``,
+  ``src/engine/attention.py:183``): ``y = bf16(x . W^T)``.
 - int8 weight-only (no reference counterpart; the reference names weight
   quantisation as future work only, reference ``DESIGN.md:120``): per output row
   ``s_r = max|w_r| / 127`` (fp32), ``q = clamp(rint(w / s_r), -127, 127)``;
@@ -177,6 +179,18 @@ def ref_qkv_full(x_bits: np.ndarray, w_bits: np.ndarray, n_q: int, n_k: int,
     return OracleOut(central.reshape(shp), lo.reshape(shp), hi.reshape(shp))
 
 
+def ref_linear(x_bits: np.ndarray, w_bits: np.ndarray, tau: float = TAU_SUM) -> OracleOut:
+    """``bf16(x . W^T)`` for a bias-free Linear: the ``down`` and ``o``
+    projections (src/engine/model.py:37, src/engine/attention.py:183, both
+    ``nn.Linear(..., bias=False)`` applied in bf16). The same contraction and
+    single rounding as the QKV output before its split."""
+    if w_bits.ndim != 2:
+        raise ValueError(f"W must be 2D (N, K), got shape {tuple(w_bits.shape)}")
+    if x_bits.shape[-1] != w_bits.shape[1]:
+        raise ValueError(f"x last dim {x_bits.shape[-1]} != W.shape[1] {w_bits.shape[1]}")
+    return ref_qkv_full(x_bits, w_bits, w_bits.shape[0], 0, tau)
+
+
 def split_qkv(y: np.ndarray, n_q: int, n_k: int):
     """(q, k, v) column blocks of y, as views (fused_qkv.py:148)."""
     return y[..., :n_q], y[..., n_q:n_q + n_k], y[..., n_q + n_k:n_q + 2 * n_k]
@@ -258,6 +272,11 @@ def dequant_w8(q: np.ndarray, s: np.ndarray) -> np.ndarray:
 def ref_qkv_w8_full(x_bits, q, s, n_q: int, n_k: int) -> OracleOut:
     """int8 QKV: dequantise then the bf16 QKV contract."""
     return ref_qkv_full(x_bits, dequant_w8(q, s), n_q, n_k)
+
+
+def ref_linear_w8(x_bits, q, s) -> OracleOut:
+    """int8 Linear: dequantise then the bf16 Linear contract."""
+    return ref_linear(x_bits, dequant_w8(q, s))
 
 
 def ref_gate_up_silu_w8_full(x_bits, qg, sg, qu, su) -> OracleOut:

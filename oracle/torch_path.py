@@ -7,6 +7,8 @@ kernels are not swapped in, restated as pure functions:
   equivalently one ``F.linear`` on the row-stacked weight then ``split``
   (``src/bench/microbench_fused_qkv.py:101-103``, ``src/kernels/fused_qkv.py:148``).
 - gate-up-SiLU: ``F.silu(self.gate(x)) * self.up(x)`` (``src/engine/model.py:37``).
+- down / o: ``self.down(...)`` (``src/engine/model.py:37``) and ``self.o(attn)``
+  (``src/engine/attention.py:183``), bias-free ``F.linear``.
 - int8 weight-only: dequantise to bf16, then the calls above (the task's
   definition; the reference has no int8 path).
 
@@ -33,6 +35,14 @@ def torch_qkv_3(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.T
 def torch_gate_up_silu(x: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor) -> torch.Tensor:
     """``F.silu(F.linear(x, Wg)) * F.linear(x, Wu)``."""
     return F.silu(F.linear(x, wg)) * F.linear(x, wu)
+
+
+def torch_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    return F.linear(x, w)
+
+
+def torch_linear_w8(x, q, s):
+    return F.linear(x, torch_dequant(q, s))
 
 
 def torch_quantize_w8(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -32,6 +32,7 @@ def test_header_declares_entry_points():
     names = _declared_functions()
     for expected in ("fp_qkv_bf16", "fp_gate_up_silu_bf16", "fp_qkv_w8",
                      "fp_gate_up_silu_w8", "fp_quantize_w8_per_row",
+                     "fp_linear_bf16", "fp_linear_w8",
                      "fp_status_string", "fp_abi_version"):
         assert expected in names
 
@@ -78,6 +79,12 @@ def test_argument_errors_return_before_launch():
     assert lib.fp_qkv_w8(P, 64, P, 64, None, P, 96, 2, 64, 16, 64, None) == 1   # NULL scale
     assert lib.fp_gate_up_silu_w8(P, 64, P, 64, P, P, 64, None, P, 32, 2, 32, 64, None) == 1
     assert lib.fp_gate_up_silu_w8(P, 64, P, 10, P, P, 64, P, P, 32, 2, 32, 64, None) == 3
+    # fp_linear_bf16(x, ldx, w, ldw, y, ldy, M, N, K, stream)
+    assert lib.fp_linear_bf16(P, 64, P, 64, P, 32, 2, 0, 64, None) == 2      # N < 1
+    assert lib.fp_linear_bf16(P, 64, P, 64, P, 31, 2, 32, 64, None) == 3     # ldy < N
+    assert lib.fp_linear_bf16(P, 64, None, 64, P, 32, 2, 32, 64, None) == 1  # NULL w
+    assert lib.fp_linear_w8(P, 64, P, 64, None, P, 32, 2, 32, 64, None) == 1  # NULL scale
+    assert lib.fp_linear_w8(P, 64, P, 63, P, P, 32, 2, 32, 64, None) == 3    # ldq < K
     assert lib.fp_quantize_w8_per_row(P, 64, P, 63, P, 8, 64, None) == 3
     assert lib.fp_quantize_w8_per_row(P, 64, P, 64, P, -1, 64, None) == 2
     assert lib.fp_quantize_w8_per_row(None, 64, None, 64, None, 0, 64, None) == 0

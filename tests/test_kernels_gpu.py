@@ -270,14 +270,15 @@ def test_split_k_regime(M, K):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 8, 5), (1, 520, 33), (1, 2536, 9701), (1, 16384, 64),
-                                   (1, 16392, 24), (1, 4096, 1), (2, 8, 7), (2, 2536, 1001),
-                                   (2, 8192, 40), (2, 8200, 24)])
+                                   (1, 16392, 24), (1, 32768, 24), (1, 32776, 16), (1, 4096, 1),
+                                   (2, 8, 7), (2, 2536, 1001), (2, 8192, 40), (2, 9728, 24),
+                                   (2, 16384, 24), (2, 16392, 16)])
 def test_row_streaming_edges(M, K, N):
     """M <= 2 bf16 runs the row-streaming kernel (one wave per weight row, K
-    in 512-element chunks, M x rows in LDS up to M * K = 16384): tiny and
-    ragged K (the last chunk partly past the row), N not a multiple of the
-    rows per workgroup, the largest K it takes and the first K it hands to
-    the streaming kernel."""
+    in 512-element chunks, M x rows in LDS up to 64 KiB, i.e. M * K <=
+    32768): tiny and ragged K (the last chunk partly past the row), N not a
+    multiple of the rows per workgroup, the largest K it takes and the first
+    K it hands to the streaming kernel."""
     n_q = max(N - 2 * (N // 4), 1)
     n_k = (N - n_q) // 2
     check_qkv(40 + K + M, M, K, n_q, n_k, label=f"qkv M={M} K={K} N={n_q + 2 * n_k}")
@@ -339,7 +340,9 @@ def test_int8_tails_and_zero_rows():
     kern = _kernels()
     for M, K, N in [(3, 2541, 100), (70, 2541, 100), (5, 1040, 48), (90, 1040, 48),
                     (1, 16, 5), (1, 1040, 33), (1, 2541, 9), (1, 16384, 20), (1, 16400, 7),
-                    (2, 1040, 33), (3, 2560, 17), (4, 4096, 9), (4, 4112, 5)]:
+                    (2, 1040, 33), (3, 2560, 17), (4, 4096, 9), (4, 4112, 5),
+                    (1, 32768, 9), (1, 32784, 5), (2, 16384, 7), (2, 16400, 5),
+                    (3, 8192, 5), (4, 8192, 9), (4, 8208, 5)]:
         x, wg, wu = ffn_inputs(M + K, M, K, N)
         wg[3] = 0  # an all-zero row: s = 0, q = 0
         qg, sg = _quant(wg)
@@ -371,6 +374,64 @@ def test_qwen3_8b_int8(M):
     out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
                                        qu.cpu().numpy(), su.cpu().numpy())
     _check(y[rows], out, f"8B int8 gate-up M={M}")
+
+
+# ----- plain projections: down and o (bias-free Linear) ----------------------
+
+
+def check_linear(seed, M, K, N, label=""):
+    x, w = qkv_inputs(seed, M, K, N, 0)
+    y = _kernels().fused_linear(x.to(DEV), w.to(DEV)).cpu()
+    rows = _rows(M)
+    return _check(y[rows], ref.ref_linear(bits(x)[rows], bits(w)), label or f"linear M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16, 64, 256, 512, 2048])
+@pytest.mark.parametrize("K,N", [(9728, 2560), (4096, 2560)], ids=["4b-down", "4b-o"])
+def test_linear_down_o(M, K, N):
+    """The Qwen3-4B down (K = intermediate) and o (K = heads * head_dim)
+    projections across the regimes: row streaming, split-K, LDS tiles."""
+    check_linear(100 + M, M, K, N, label=f"linear K={K} N={N} M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 16, 4096])
+def test_linear_8b_down(M):
+    check_linear(110 + M, M, 12288, 4096, label=f"8B down M={M}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 8, 3), (1, 203, 33), (3, 200, 33), (9, 1040, 100),
+                                   (70, 2536, 130), (300, 1001, 77)])
+def test_linear_tails(M, K, N):
+    """Ragged K and N in every regime, including K not a multiple of 8 (the
+    unaligned streaming path)."""
+    check_linear(120 + M, M, K, N)
+
+
+@pytest.mark.parametrize("M", [1, 4, 64, 2048])
+def test_linear_int8(M):
+    K, N = 9728, 2560
+    x, w = qkv_inputs(130 + M, M, K, N, 0)
+    q, s = _quant(w)
+    y = _kernels().fused_linear_w8(x.to(DEV), q, s).cpu()
+    rows = _rows(M)
+    out = ref.ref_linear_w8(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy())
+    _check(y[rows], out, f"int8 down M={M}")
+
+
+def test_linear_errors_and_leading_dims():
+    kern = _kernels()
+    x, w = qkv_inputs(140, 6, 256, 96, 0)
+    y = kern.fused_linear(x.view(2, 3, 256).to(DEV), w.to(DEV))
+    assert y.shape == (2, 3, 96)
+    _check(y.reshape(6, 96).cpu(), ref.ref_linear(bits(x), bits(w)), "linear leading dims")
+    assert kern.fused_linear(x[:0].to(DEV), w.to(DEV)).shape == (0, 96)
+    with pytest.raises(ValueError, match="x last dim"):
+        kern.fused_linear(x[:, :-8].to(DEV), w.to(DEV))
+    with pytest.raises(TypeError, match="bfloat16"):
+        kern.fused_linear(x.float().to(DEV), w.to(DEV))
+    q, s = _quant(w)
+    with pytest.raises(ValueError, match="s shape"):
+        kern.fused_linear_w8(x.to(DEV), q, s[:-1])
 
 
 # ----- size-independent properties at full size ------------------------------

@@ -28,7 +28,8 @@ import pytest
 import torch
 from torch import nn
 
-from llms_amd.kernels import TritonAttention, TritonFFN, apply_triton_kernels, prewarm_triton_kernels
+from llms_amd.kernels import (FusedLinear, TritonAttention, TritonFFN, apply_triton_kernels,
+                              prewarm_triton_kernels)
 from tests._tiny_qwen3 import Cfg, greedy_generate, teacher_forced_logits, tiny_model, tiny_state
 
 DEV = "cuda"
@@ -98,6 +99,32 @@ def test_apply_respects_flags():
     assert all(isinstance(b.ffn, TritonFFN) for b in m.layers)
 
 
+def test_apply_linear_down_o_swaps_and_keeps_keys():
+    """``linear_down_o=True`` replaces every ``ffn.down`` and ``attn.o`` with
+    a FusedLinear sharing the Linear's weight (same state keys), once."""
+    m = tiny_model(TINY, device="cpu")
+    eager_keys = set(m.state_dict())
+    downs = [b.ffn.down.weight for b in m.layers]
+    apply_triton_kernels(m, linear_down_o=True)
+    assert all(isinstance(b.ffn.down, FusedLinear) and isinstance(b.attn.o, FusedLinear)
+               for b in m.layers)
+    assert all(w is b.ffn.down.weight for w, b in zip(downs, m.layers, strict=True))
+    first = [(b.ffn.down, b.attn.o) for b in m.layers]
+    apply_triton_kernels(m, linear_down_o=True)
+    assert all(d is b.ffn.down and o is b.attn.o for (d, o), b in zip(first, m.layers, strict=True))
+    keys = set(m.state_dict())
+    for i in range(TINY.num_hidden_layers):
+        for k in (f"layers.{i}.ffn.down.weight", f"layers.{i}.attn.o.weight"):
+            assert k in eager_keys and k in keys
+    # only down/o: the flag works without the fused projections too
+    m = apply_triton_kernels(tiny_model(TINY, device="cpu"), fused_ffn=False, fused_qkv=False,
+                             linear_down_o=True)
+    assert all(isinstance(b.ffn.down, FusedLinear) and not isinstance(b.ffn, TritonFFN)
+               for b in m.layers)
+    with pytest.raises(ValueError):
+        FusedLinear.from_linear(nn.Linear(4, 4, bias=True))
+
+
 def test_prewarm_no_op_without_fused_modules():
     """Reference ``test_kernels_fused_ffn.py:395-406``: a model with no
     fused modules (and no ``.layers``) is walked without error."""
@@ -122,15 +149,17 @@ def _logit_tol(ref: torch.Tensor) -> float:
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("which", ["ffn", "qkv", "both"])
+@pytest.mark.parametrize("which", ["ffn", "qkv", "both", "all"])
 @pytest.mark.parametrize("c", [TINY, WIDE], ids=["tiny", "wide"])
 def test_module_logits_match(which, c):
     """Prefill logits of the swapped model agree with the eager model and the
     last-token argmax is equal (reference ``test_ffn_module_logits_match``,
-    ``test_attention_module_logits_match``)."""
+    ``test_attention_module_logits_match``); "all" also runs down and o on
+    the HIP kernels."""
     kw = {"ffn": dict(fused_ffn=True, fused_qkv=False),
           "qkv": dict(fused_ffn=False, fused_qkv=True),
-          "both": dict(fused_ffn=True, fused_qkv=True)}[which]
+          "both": dict(fused_ffn=True, fused_qkv=True),
+          "all": dict(fused_ffn=True, fused_qkv=True, linear_down_o=True)}[which]
     eager, fused = _pair(c, **kw)
     assert all(isinstance(b.ffn, TritonFFN) == kw["fused_ffn"] for b in fused.layers)
     assert all(isinstance(b.attn, TritonAttention) == kw["fused_qkv"] for b in fused.layers)
@@ -162,7 +191,7 @@ def test_apply_idempotent_on_device():
 def test_prewarm_runs_clean(int8):
     """prewarm leaves forward outputs bit-identical (reference
     ``test_prewarm_runs_clean``)."""
-    m = apply_triton_kernels(tiny_model(TINY, device=DEV), int8=int8)
+    m = apply_triton_kernels(tiny_model(TINY, device=DEV), int8=int8, linear_down_o=True)
     ids = torch.tensor([[1, 20, 3, 14, 5, 26, 7, 18]], device=DEV)
     before = _logits(m, ids, 32)
     prewarm_triton_kernels(m)
@@ -215,18 +244,23 @@ def test_greedy_token_match(c, prompt):
 
 
 @pytest.mark.gpu
-def test_int8_model_matches_dequantised_eager():
+@pytest.mark.parametrize("down_o", [False, True], ids=["qkv-ffn", "all"])
+def test_int8_model_matches_dequantised_eager(down_o):
     """``apply_triton_kernels(int8=True)``: logits match an eager model whose
-    q/k/v/gate/up weights are replaced by their dequantised bf16(q * s)."""
+    q/k/v/gate/up (and with ``linear_down_o``, down/o) weights are replaced
+    by their dequantised bf16(q * s)."""
     from llms_amd.kernels import dequantize_w8, quantize_w8_per_row
 
     c = WIDE
     st = tiny_state(c, seed=3)
-    fused = apply_triton_kernels(tiny_model(c, state=st, device=DEV), int8=True)
+    fused = apply_triton_kernels(tiny_model(c, state=st, device=DEV), int8=True,
+                                 linear_down_o=down_o)
     deq = dict(st)
+    names = ("attn.q.weight", "attn.k.weight", "attn.v.weight", "ffn.gate.weight", "ffn.up.weight")
+    if down_o:
+        names += ("ffn.down.weight", "attn.o.weight")
     for k, v in st.items():
-        if k.endswith(("attn.q.weight", "attn.k.weight", "attn.v.weight",
-                       "ffn.gate.weight", "ffn.up.weight")):
+        if k.endswith(names):
             q, s = quantize_w8_per_row(v.to(torch.bfloat16).to(DEV))
             deq[k] = dequantize_w8(q, s).float().cpu()
     eager = tiny_model(c, state=deq, device=DEV)

@@ -169,6 +169,21 @@ def test_gate_up_fp32_contract_matches_nn_modules():
     np.testing.assert_allclose(got, expect, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 9728, 64), (4, 4096, 96), (7, 200, 33)])
+def test_linear_matches_torch_bf16_linear(M, K, N):
+    """The down/o contract: torch's CPU bf16 F.linear (reference model.py:37,
+    attention.py:183) lands inside the oracle's hull everywhere."""
+    x, w = qkv_inputs(16, M, K, N, 0)
+    out = ref.ref_linear(bits(x), bits(w))
+    p = _hull_contains(bits(tp.torch_linear(x, w)), out)
+    assert p.n_outside == 0, p
+    assert p.n_differ <= max(2, p.n // 200), p
+    qw, sw = tp.torch_quantize_w8(w)
+    out = ref.ref_linear_w8(bits(x), qw.numpy(), sw.numpy())
+    p = _hull_contains(bits(tp.torch_linear_w8(x, qw, sw)), out)
+    assert p.n_outside == 0, p
+
+
 # ------------------------------------------------------------- brute force
 
 
@@ -185,6 +200,19 @@ def test_qkv_exact_rational_bruteforce():
         for n in range(16):
             s = sum(a * b for a, b in zip(xf[m], wf[n]))
             assert Fraction(float(out.central[m, n])) == exact_round_bf16(s)
+
+
+def test_linear_exact_rational_bruteforce():
+    x, w = qkv_inputs(17, 2, 24, 10, 0, w_std=0.3)
+    xb, wb = bits(x), bits(w)
+    xf, wf = _frac(xb), _frac(wb)
+    out = ref.ref_linear(xb, wb)
+    for m in range(2):
+        for n in range(10):
+            s = sum(a * b for a, b in zip(xf[m], wf[n]))
+            assert Fraction(float(out.central[m, n])) == exact_round_bf16(s)
+    with pytest.raises(ValueError, match="x last dim"):
+        ref.ref_linear(xb[:, :-1], wb)
 
 
 def test_gate_up_exact_rational_bruteforce():
