@@ -17,7 +17,9 @@
  *     stride in ELEMENTS. Weights use the nn.Linear layout [N, K].
  *   - stream is a hipStream_t (NULL = the legacy default stream). Every call
  *     is asynchronous on that stream; nothing is allocated, freed or
- *     synchronised; no global state is written; calls are reentrant.
+ *     synchronised; no global state is written; calls are reentrant. The
+ *     *_ws variants also write the caller's workspace, which must not be
+ *     used by work that can overlap the call.
  *   - Return 0 (FP_OK) on success, a nonzero fp_status otherwise; argument
  *     errors are detected before anything is launched.
  *   - Results are deterministic: the same inputs give bit-identical outputs
@@ -48,7 +50,8 @@ typedef enum fp_status {
   FP_ERR_SHAPE = 2,      /* M, N, K, n_q, n_k out of range or inconsistent */
   FP_ERR_STRIDE = 3,     /* a row stride is smaller than the row length */
   FP_ERR_LAUNCH = 4,     /* the HIP launch reported an error */
-  FP_ERR_DEVICE = 5      /* no usable gfx950 device for the current context */
+  FP_ERR_DEVICE = 5,     /* no usable gfx950 device for the current context */
+  FP_ERR_WORKSPACE = 6   /* workspace not 16-byte aligned, or a negative size */
 } fp_status;
 
 /* Human-readable text for an fp_status value (static storage). */
@@ -125,6 +128,42 @@ int fp_linear_w8(const void* x, int64_t ldx,
                  void* y, int64_t ldy,
                  int64_t M, int64_t N, int64_t K,
                  void* stream);
+
+/*
+ * Workspace variants of the three bf16 entry points (no reference
+ * counterpart: the reference's Triton launches take no workspace). With a
+ * workspace of at least fp_workspace_bytes(M, N, K, gate_up) bytes
+ * (N = n_q + 2*n_k for QKV, the output width otherwise), calls whose tile
+ * grid would leave CUs idle while each tile runs a long k loop split k across
+ * workgroups: fp32 partial sums go to the workspace and a second kernel sums
+ * them in a fixed order and applies the epilogue (results stay
+ * deterministic). A NULL or smaller workspace runs the unsplit kernels of the
+ * plain entry points. The workspace must be 16-byte aligned (any hipMalloc or
+ * torch allocation is) and is overwritten.
+ */
+int64_t fp_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up);
+
+int fp_qkv_bf16_ws(const void* x, int64_t ldx,
+                   const void* w, int64_t ldw,
+                   void* y, int64_t ldy,
+                   int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+                   void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
+int fp_gate_up_silu_bf16_ws(const void* x, int64_t ldx,
+                            const void* wg, int64_t ldwg,
+                            const void* wu, int64_t ldwu,
+                            void* y, int64_t ldy,
+                            int64_t M, int64_t N, int64_t K,
+                            void* workspace, int64_t workspace_bytes,
+                            void* stream);
+
+int fp_linear_bf16_ws(const void* x, int64_t ldx,
+                      const void* w, int64_t ldw,
+                      void* y, int64_t ldy,
+                      int64_t M, int64_t N, int64_t K,
+                      void* workspace, int64_t workspace_bytes,
+                      void* stream);
 
 /*
  * Per-output-channel symmetric int8 quantisation on the device (the packing

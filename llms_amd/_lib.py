@@ -39,6 +39,10 @@ CAPI_SIGNATURES: dict[str, list] = {
     "fp_linear_bf16": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "fp_linear_w8": [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P],
     "fp_quantize_w8_per_row": [_P, _I64, _P, _I64, _P, _I64, _I64, _P],
+    "fp_workspace_bytes": [_I64, _I64, _I64, ctypes.c_int],
+    "fp_qkv_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "fp_gate_up_silu_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "fp_linear_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
 }
 
 FP_STATUS = {
@@ -48,6 +52,7 @@ FP_STATUS = {
     3: "FP_ERR_STRIDE",
     4: "FP_ERR_LAUNCH",
     5: "FP_ERR_DEVICE",
+    6: "FP_ERR_WORKSPACE",
 }
 
 
@@ -69,7 +74,8 @@ def capi() -> ctypes.CDLL:
             for name, argtypes in CAPI_SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
-                fn.restype = ctypes.c_char_p if name == "fp_status_string" else ctypes.c_int
+                fn.restype = {"fp_status_string": ctypes.c_char_p,
+                              "fp_workspace_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
             _capi = lib
         return _capi
 

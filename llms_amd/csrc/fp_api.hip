@@ -75,41 +75,64 @@ const char* fp_status_string(int status) {
     case FP_ERR_STRIDE: return "row stride smaller than the row length";
     case FP_ERR_LAUNCH: return "HIP kernel launch failed";
     case FP_ERR_DEVICE: return "no gfx950 code object for the current device";
+    case FP_ERR_WORKSPACE: return "workspace not 16-byte aligned, or a negative workspace size";
     default: return "unknown fp_status";
   }
 }
 
-int fp_abi_version(void) { return (1 << 16) | 1; }
+int fp_abi_version(void) { return (1 << 16) | 2; }
 
-int fp_qkv_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
-                int64_t M, int64_t n_q, int64_t n_k, int64_t K, void* stream) {
+int64_t fp_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up) {
+  if (M < 1 || N < 1 || K < 1) return 0;
+  const fp::GemmSplit p = fp::gemm_split_plan(M, N, K, gate_up != 0);
+  return 4 * fp::gemm_split_ws_floats(p, M, N, K, gate_up != 0);
+}
+
+int fp_qkv_bf16_ws(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                   int64_t M, int64_t n_q, int64_t n_k, int64_t K, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
   if (n_q < 1 || n_k < 0) return FP_ERR_SHAPE;
   const int64_t N = n_q + 2 * n_k;
   int st = fp::check_common(M, N, K, ldx, ldy);
   if (st) return st;
   if (ldw < K) return FP_ERR_STRIDE;
+  if (workspace_bytes < 0 || (workspace && !fp::al16(workspace))) return FP_ERR_WORKSPACE;
   if (M == 0) return FP_OK;
   if (!x || !w || !y) return FP_ERR_NULL;
   StreamArgs a{(const uint16_t*)x, ldx, w, ldw, nullptr, 0, nullptr, nullptr,
-               (uint16_t*)y, ldy, M, N, K};
+               (uint16_t*)y, ldy, M, N, K, (float*)workspace, workspace_bytes / 4};
   const bool aligned = (K % 8 == 0) && (ldx % 8 == 0) && (ldw % 8 == 0) &&
                        fp::al16(x) && fp::al16(w);
   return fp::run<false, false>(a, aligned, (hipStream_t)stream);
 }
 
-int fp_gate_up_silu_bf16(const void* x, int64_t ldx, const void* wg, int64_t ldwg,
-                         const void* wu, int64_t ldwu, void* y, int64_t ldy,
-                         int64_t M, int64_t N, int64_t K, void* stream) {
+int fp_qkv_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
+                int64_t M, int64_t n_q, int64_t n_k, int64_t K, void* stream) {
+  return fp_qkv_bf16_ws(x, ldx, w, ldw, y, ldy, M, n_q, n_k, K, nullptr, 0, stream);
+}
+
+int fp_gate_up_silu_bf16_ws(const void* x, int64_t ldx, const void* wg, int64_t ldwg,
+                            const void* wu, int64_t ldwu, void* y, int64_t ldy, int64_t M,
+                            int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                            void* stream) {
   int st = fp::check_common(M, N, K, ldx, ldy);
   if (st) return st;
   if (ldwg < K || ldwu < K) return FP_ERR_STRIDE;
+  if (workspace_bytes < 0 || (workspace && !fp::al16(workspace))) return FP_ERR_WORKSPACE;
   if (M == 0) return FP_OK;
   if (!x || !wg || !wu || !y) return FP_ERR_NULL;
   StreamArgs a{(const uint16_t*)x, ldx, wg, ldwg, wu, ldwu, nullptr, nullptr,
-               (uint16_t*)y, ldy, M, N, K};
+               (uint16_t*)y, ldy, M, N, K, (float*)workspace, workspace_bytes / 4};
   const bool aligned = (K % 8 == 0) && (ldx % 8 == 0) && (ldwg % 8 == 0) && (ldwu % 8 == 0) &&
                        fp::al16(x) && fp::al16(wg) && fp::al16(wu);
   return fp::run<true, false>(a, aligned, (hipStream_t)stream);
+}
+
+int fp_gate_up_silu_bf16(const void* x, int64_t ldx, const void* wg, int64_t ldwg,
+                         const void* wu, int64_t ldwu, void* y, int64_t ldy,
+                         int64_t M, int64_t N, int64_t K, void* stream) {
+  return fp_gate_up_silu_bf16_ws(x, ldx, wg, ldwg, wu, ldwu, y, ldy, M, N, K, nullptr, 0,
+                                 stream);
 }
 
 int fp_qkv_w8(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,
@@ -147,6 +170,12 @@ int fp_gate_up_silu_w8(const void* x, int64_t ldx, const int8_t* qg, int64_t ldq
 int fp_linear_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
                    int64_t M, int64_t N, int64_t K, void* stream) {
   return fp_qkv_bf16(x, ldx, w, ldw, y, ldy, M, N, 0, K, stream);
+}
+
+int fp_linear_bf16_ws(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
+  return fp_qkv_bf16_ws(x, ldx, w, ldw, y, ldy, M, N, 0, K, workspace, workspace_bytes, stream);
 }
 
 int fp_linear_w8(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,

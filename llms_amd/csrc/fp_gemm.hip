@@ -48,8 +48,13 @@ __device__ __forceinline__ void load_lds16(const void* base, int nbytes, lds_ptr
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= v only.
 constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >> 4) << 14); }
 
-template <int BN, int BM, int WN, int WM, bool GATEUP, int NS>
-__global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int n_mt, int n_nt) {
+// SPLIT: the grid holds nsplit workgroups per tile, each contracting one
+// contiguous range of k-steps, and the fp32 accumulators go to the workspace
+// ws[split][m][col] (col: output column n; gate-up: g at n, u at N + n) for
+// splitk_reduce_kernel, which sums them in split order.
+template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool SPLIT = false>
+__global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int n_mt, int n_nt,
+                                                              int ksteps, float* ws) {
   constexpr int NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;   // per-wave tile
   constexpr int FN = TN / 16, FM = TM / 16;   // MFMA sub-tiles per wave
@@ -77,10 +82,13 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   const int wn = wave / WM, wm = wave % WM;
   const int li = lane & 15, grp = lane >> 4;
 
-  // XCD-aware tile order (see file comment), then M-fastest within an XCD.
-  const int T = n_mt * n_nt;
+  // XCD-aware tile order (see file comment), then M-fastest within an XCD;
+  // with SPLIT the k-range index is the slowest.
+  const int T = (int)gridDim.x;
   int b = blockIdx.x;
   if (T % 8 == 0) b = (b % 8) * (T / 8) + b / 8;
+  const int ks = SPLIT ? b / (n_mt * n_nt) : 0;
+  b -= ks * n_mt * n_nt;
   const int tm = b % n_mt, tn = b / n_mt;
   const int64_t m0 = (int64_t)tm * BM;
   const int64_t c0 = (int64_t)tn * (GATEUP ? BN / 2 : BN);  // first output column
@@ -171,10 +179,13 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   // wave's loads of step k+1 have landed (the NS-2 later steps may stay in
   // flight), then for every wave's.
   constexpr int kPerStep = IW + IX;  // load instructions per wave per step
-  const int64_t nkt = a.K / kBK;
+  const int64_t kfirst = (int64_t)ks * ksteps;  // first k-step of this workgroup
+  const int64_t nleft = a.K / kBK - kfirst;
+  const int64_t nkt = SPLIT ? (ksteps < nleft ? (int64_t)ksteps : nleft) : a.K / kBK;
+  const int64_t kb0 = kfirst * kBK;
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nkt) issue(stw(s), stx(s), s * kBK);
+    if (s < nkt) issue(stw(s), stx(s), kb0 + s * kBK);
   if (nkt > NS - 2)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * kPerStep));
   else
@@ -186,7 +197,7 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
       const int64_t k = kt + u;
       if (k >= nkt) break;
       const bool steady = k + NS - 1 < nkt;
-      if (steady) issue(stw((u + NS - 1) % NS), stx((u + NS - 1) % NS), (k + NS - 1) * kBK);
+      if (steady) issue(stw((u + NS - 1) % NS), stx((u + NS - 1) % NS), kb0 + (k + NS - 1) * kBK);
       compute(stw(u), stx(u));
       if (steady)
         __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * kPerStep));
@@ -194,6 +205,38 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       __syncthreads();
     }
+  }
+
+  if constexpr (SPLIT) {
+    // fp32 partials: 4 consecutive columns of one x row per lane
+    const int64_t wc = GATEUP ? 2 * a.N : a.N;
+    const bool v16 = (wc & 3) == 0;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int64_t m = m0 + wm * TM + j * 16 + li;
+      if (m >= a.M) continue;
+      float* prow = ws + ((int64_t)ks * a.M + m) * wc;
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        int64_t n, col;
+        if constexpr (GATEUP) {
+          const int sub = (wn * TN) / 16 + i;  // even: gate rows, odd: up rows
+          n = c0 + (sub / 2) * 16 + 4 * grp;
+          col = (sub & 1) ? a.N + n : n;
+        } else {
+          n = c0 + wn * TN + i * 16 + 4 * grp;
+          col = n;
+        }
+        if (v16 && n + 3 < a.N) {
+          *reinterpret_cast<f32x4*>(prow + col) = acc[i][j];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < a.N) prow[col + r] = acc[i][j][r];
+        }
+      }
+    }
+    return;
   }
 
   // ---- epilogue ----
@@ -228,6 +271,51 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   }
 }
 
+// Sums the nsplit partial accumulators of each output in split order 0, 1,
+// ... (a fixed order: results do not depend on scheduling) and applies the
+// epilogue at the torch rounding points. One thread per 4 columns of a row.
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int nsplit,
+                                                            StreamArgs a) {
+  const int64_t nq = (a.N + 3) / 4;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= a.M * nq) return;
+  const int64_t m = t / nq, n = (t - m * nq) * 4;
+  const int64_t wc = GATEUP ? 2 * a.N : a.N;
+  const int64_t plane = a.M * wc;  // floats per split
+  const float* p = ws + m * wc + n;
+  uint32_t h[4];
+  if ((wc & 3) == 0 && n + 3 < a.N) {
+    f32x4 g = *reinterpret_cast<const f32x4*>(p);
+    f32x4 u = GATEUP ? *reinterpret_cast<const f32x4*>(p + a.N) : f32x4{};
+    for (int s = 1; s < nsplit; ++s) {
+      g += *reinterpret_cast<const f32x4*>(p + s * plane);
+      if constexpr (GATEUP) u += *reinterpret_cast<const f32x4*>(p + s * plane + a.N);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) h[r] = GATEUP ? gate_up_silu_bits(g[r], u[r]) : f32_to_bf16_bits(g[r]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (n + r >= a.N) break;
+      float g = p[r], u = GATEUP ? p[r + a.N] : 0.f;
+      for (int s = 1; s < nsplit; ++s) {
+        g += p[s * plane + r];
+        if constexpr (GATEUP) u += p[s * plane + r + a.N];
+      }
+      h[r] = GATEUP ? gate_up_silu_bits(g, u) : f32_to_bf16_bits(g);
+    }
+  }
+  uint16_t* yrow = a.y + m * a.ldy;
+  if (((a.ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 7) == 0) && n + 3 < a.N) {
+    *reinterpret_cast<u32x2*>(yrow + n) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < a.N) yrow[n + r] = (uint16_t)h[r];
+  }
+}
+
 }  // namespace
 
 template <int BN, int BM, int WN, int WM, bool GATEUP, int NS>
@@ -236,7 +324,42 @@ int launch_gemm_cfg(const StreamArgs& a, hipStream_t s) {
   const int n_nt = (int)((a.N + cols - 1) / cols);
   const int n_mt = (int)((a.M + BM - 1) / BM);
   hipLaunchKernelGGL((gemm_kernel<BN, BM, WN, WM, GATEUP, NS>), dim3((unsigned)(n_nt * n_mt)),
-                     dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt);
+                     dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt, 0, (float*)nullptr);
+  return (int)hipGetLastError();
+}
+
+// Split-K form: at most `nsplit` k-ranges of whole k-steps per tile (the
+// count actually used, every range non-empty, is returned through
+// *used_split), partials in ws (gemm_splitk_ws_floats floats), then the
+// reduce kernel.
+inline int64_t gemm_splitk_ksteps(int64_t K, int nsplit) {
+  const int64_t nkt = K / kBK;
+  return (nkt + nsplit - 1) / nsplit;
+}
+inline int gemm_splitk_used(int64_t K, int nsplit) {
+  const int64_t per = gemm_splitk_ksteps(K, nsplit);
+  return (int)((K / kBK + per - 1) / per);
+}
+template <bool GATEUP>
+int64_t gemm_splitk_ws_floats(const StreamArgs& a, int nsplit) {
+  return (int64_t)gemm_splitk_used(a.K, nsplit) * a.M * (GATEUP ? 2 * a.N : a.N);
+}
+
+template <int BN, int BM, int WN, int WM, bool GATEUP, int NS>
+int launch_gemm_splitk_cfg(const StreamArgs& a, int nsplit, float* ws, hipStream_t s) {
+  const int64_t cols = GATEUP ? BN / 2 : BN;
+  const int n_nt = (int)((a.N + cols - 1) / cols);
+  const int n_mt = (int)((a.M + BM - 1) / BM);
+  const int per = (int)gemm_splitk_ksteps(a.K, nsplit);
+  const int used = gemm_splitk_used(a.K, nsplit);
+  hipLaunchKernelGGL((gemm_kernel<BN, BM, WN, WM, GATEUP, NS, true>),
+                     dim3((unsigned)(n_nt * n_mt * used)), dim3(WN * WM * kWave), 0, s, a, n_mt,
+                     n_nt, per, ws);
+  int e = (int)hipGetLastError();
+  if (e) return e;
+  const int64_t threads = a.M * ((a.N + 3) / 4);
+  hipLaunchKernelGGL(splitk_reduce_kernel<GATEUP>, dim3((unsigned)((threads + 255) / 256)),
+                     dim3(256), 0, s, ws, used, a);
   return (int)hipGetLastError();
 }
 
@@ -253,35 +376,112 @@ bool gemm_supported(const StreamArgs& a, bool aligned) {
   return true;
 }
 
-// Tile table for the bf16 prefill path, measured on MI355X with Qwen3-4B and
-// -8B shapes. What decides is how many rounds of workgroups a call needs on
-// 256 CUs: 256 x 256 tiles (1 workgroup per CU) run best once they fill the
-// chip, smaller tiles (2 per CU) win where they save a round. QKV-sized
-// outputs (<= 8192 weight rows): 64 x 128 tiles with three stages to 768 rows,
-// 128 x 128 to 1536, then 256 x 256. Outputs of at most 4096 columns (the
-// down and o projections) keep 128 x 128 to 4096 rows: a 256 x 256 grid
-// there is under one round (2048 x 2560 -> 80 tiles). Gate-up-sized: 128 x
-// 128 to 384 rows, 256 x 256 to 768 (152-192 tiles, one round), 128 x 128 to
-// 1536, 256 x 256.
-template <bool GATEUP>
-int launch_gemm(const StreamArgs& a, hipStream_t s) {
-  const int64_t wrows = GATEUP ? 2 * a.N : a.N;
-  if (wrows <= 4096) {
-    if (a.M <= 768) return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
-    if (a.M <= 4096) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
-    return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
-  }
-  if (wrows <= 8192) {
-    if (a.M <= 768) return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
-    if (a.M <= 1536) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
-    return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
-  }
-  if (a.M <= 384) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
-  if (a.M <= 768) return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
-  if (a.M <= 1536) return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
-  return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
+// Tiles the dispatcher uses: {weight rows, x rows, workgroups per CU (LDS)}.
+enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256 };
+struct TileInfo {
+  int bn, bm, per_cu;
+};
+constexpr TileInfo kTiles[] = {{64, 32, 4}, {128, 64, 3}, {64, 128, 2}, {128, 128, 2}, {256, 256, 1}};
+constexpr int kCUs = 256;
+
+int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
+  const int64_t cols = gateup ? kTiles[tile].bn / 2 : kTiles[tile].bn;
+  return ((N + cols - 1) / cols) * ((M + kTiles[tile].bm - 1) / kTiles[tile].bm);
 }
 
+// Tile table for the unsplit bf16 prefill path, measured on MI355X with
+// Qwen3-4B and -8B shapes. What decides is how many rounds of workgroups a
+// call needs on 256 CUs: 256 x 256 tiles (1 workgroup per CU) run best once
+// they fill the chip, smaller tiles (2 per CU) win where they save a round.
+// QKV-sized outputs (<= 8192 weight rows): 64 x 128 tiles with three stages
+// to 768 rows, 128 x 128 to 1536, then 256 x 256. Outputs of at most 4096
+// columns (the down and o projections) keep 128 x 128 to 4096 rows: a 256 x
+// 256 grid there is under one round (2048 x 2560 -> 80 tiles). Gate-up-sized:
+// 128 x 128 to 384 rows, 256 x 256 to 768 (152-192 tiles, one round), 128 x
+// 128 to 1536, 256 x 256.
+int gemm_tile_unsplit(int64_t M, int64_t wrows) {
+  if (wrows <= 4096) return M <= 768 ? kT64x128 : (M <= 4096 ? kT128x128 : kT256x256);
+  if (wrows <= 8192) return M <= 768 ? kT64x128 : (M <= 1536 ? kT128x128 : kT256x256);
+  if (M <= 384) return kT128x128;
+  if (M <= 768) return kT256x256;
+  return M <= 1536 ? kT128x128 : kT256x256;
+}
+
+template <bool GATEUP>
+int launch_gemm(const StreamArgs& a, hipStream_t s) {
+  switch (gemm_tile_unsplit(a.M, GATEUP ? 2 * a.N : a.N)) {
+    case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
+    case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
+    default: return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
+  }
+}
+
+// When to split k across workgroups, measured on MI355X over Qwen3-0.6B/4B/8B
+// QKV, gate-up, o and down shapes (M = 16..4096). Splitting pays when the
+// unsplit grid leaves CUs idle and each tile has a long k loop; it costs the
+// fp32 partials' round trip and a second launch. Rules:
+//   - at least 32 k-steps (K >= 2048) and 32 x rows (more than 32 rows for
+//     outputs wider than 4096 weight rows);
+//   - below 128 rows (the weight-streaming regime) only against large
+//     weights: >= 64 k-steps and >= 2^24 weight elements (down, 8B o);
+//   - from 128 rows while the unsplit grid fills at most half of the
+//     chip's workgroup slots, or three quarters with >= 128 k-steps; gate-up
+//     (two partial planes) only with >= 128 k-steps.
+// Tile by rows: 64 x 32 to 32 rows, 128 x 64 to 128, 128 x 128 (64 x 128
+// for outputs of at most 1024 columns) to 1024 rows or narrow outputs,
+// 256 x 256 above; splits = slots / tiles rounded, in 2..16 with at least
+// 8 k-steps each.
+GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
+  const GemmSplit none{-1, 1};
+  if (M < 32 || K % kBK != 0) return none;
+  const int64_t nkt = K / kBK, wrows = gateup ? 2 * N : N;
+  if (nkt < 32) return none;
+  if (M <= 32 && wrows > 4096) return none;
+  if (M < 128) {
+    if (nkt < 64 || wrows * K < ((int64_t)1 << 24)) return none;
+  } else {
+    if (gateup && nkt < 128) return none;
+    const int t0 = gemm_tile_unsplit(M, wrows);
+    const double fill = (double)tile_count(t0, M, N, gateup) / (kCUs * kTiles[t0].per_cu);
+    if (!(fill <= 0.5 || (fill < 0.75 && nkt >= 128))) return none;
+  }
+  int tile;
+  if (M <= 32) tile = kT64x32;
+  else if (M <= 128) tile = kT128x64;
+  else if (M <= 1024 || wrows <= 2048) tile = wrows <= 1024 ? kT64x128 : kT128x128;
+  else tile = kT256x256;
+  const double want = (double)(kCUs * kTiles[tile].per_cu) / tile_count(tile, M, N, gateup);
+  int64_t ns = (int64_t)(want + 0.5);
+  ns = ns < 16 ? ns : 16;
+  ns = ns < nkt / 8 ? ns : nkt / 8;
+  if (ns < 2) return none;
+  return GemmSplit{tile, gemm_splitk_used(K, (int)ns)};
+}
+
+int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K, bool gateup) {
+  if (p.tile < 0) return 0;
+  return (int64_t)gemm_splitk_used(K, p.nsplit) * M * (gateup ? 2 * N : N);
+}
+
+bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p) {
+  if (!a.ws || !gemm_supported(a, aligned)) return false;
+  *p = gemm_split_plan(a.M, a.N, a.K, gateup);
+  return p->tile >= 0 && gemm_split_ws_floats(*p, a.M, a.N, a.K, gateup) <= a.ws_floats;
+}
+
+template <bool GATEUP>
+int launch_gemm_split(const StreamArgs& a, const GemmSplit& p, hipStream_t s) {
+  switch (p.tile) {
+    case kT64x32: return launch_gemm_splitk_cfg<64, 32, 2, 2, GATEUP, 3>(a, p.nsplit, a.ws, s);
+    case kT128x64: return launch_gemm_splitk_cfg<128, 64, 4, 2, GATEUP, 2>(a, p.nsplit, a.ws, s);
+    case kT64x128: return launch_gemm_splitk_cfg<64, 128, 2, 2, GATEUP, 3>(a, p.nsplit, a.ws, s);
+    case kT128x128: return launch_gemm_splitk_cfg<128, 128, 4, 2, GATEUP, 2>(a, p.nsplit, a.ws, s);
+    default: return launch_gemm_splitk_cfg<256, 256, 4, 2, GATEUP, 2>(a, p.nsplit, a.ws, s);
+  }
+}
+
+template int launch_gemm_split<false>(const StreamArgs&, const GemmSplit&, hipStream_t);
+template int launch_gemm_split<true>(const StreamArgs&, const GemmSplit&, hipStream_t);
 template int launch_gemm<false>(const StreamArgs&, hipStream_t);
 template int launch_gemm<true>(const StreamArgs&, hipStream_t);
 #endif

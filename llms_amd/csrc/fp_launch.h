@@ -22,6 +22,10 @@ struct StreamArgs {
   uint16_t* y;
   int64_t ldy;
   int64_t M, N, K;
+  // Optional caller workspace for the cross-workgroup split-K contraction
+  // (16-byte aligned; NULL / too small: the unsplit kernels run).
+  float* ws;
+  int64_t ws_floats;
 };
 
 // Weight-streaming kernels (M <= 64). Return the launch's hipError_t.
@@ -46,11 +50,12 @@ int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s);
 // Split-K bf16 MFMA tiles for the middle regime (fp_splitk.hip): used by
 // launch_stream from kSplitkMinM rows (kSplitkMinMSmallN for calls with at
 // most kSplitkSmallN weight rows) and by launch_tiled for small-N calls up to
-// kSplitkMaxM rows, when splitk_supported() holds.
+// kSplitkMaxM rows with K >= kSplitkMinKTiled, when splitk_supported() holds.
 constexpr int64_t kSplitkMinM = 8;
 constexpr int64_t kSplitkMinMSmallN = 3;
 constexpr int64_t kSplitkSmallN = 8192;
 constexpr int64_t kSplitkMaxM = 256;
+constexpr int64_t kSplitkMinKTiled = 2048;
 bool splitk_supported(const StreamArgs& a, bool aligned);
 template <bool GATEUP>
 int launch_splitk(const StreamArgs& a, hipStream_t s);
@@ -60,6 +65,20 @@ int launch_splitk(const StreamArgs& a, hipStream_t s);
 bool gemm_supported(const StreamArgs& a, bool aligned);
 template <bool GATEUP>
 int launch_gemm(const StreamArgs& a, hipStream_t s);
+// k split across workgroups — for calls whose tile grid leaves the chip
+// partly idle while each tile has a long k loop — with fp32 partials in the
+// caller's workspace and a fixed-order reduce (fp_gemm.hip). tile < 0: no
+// split for this shape.
+struct GemmSplit {
+  int tile;
+  int nsplit;
+};
+GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup);
+int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K, bool gateup);
+// Whether the bf16 call a runs split (plan + workspace large enough).
+bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p);
+template <bool GATEUP>
+int launch_gemm_split(const StreamArgs& a, const GemmSplit& p, hipStream_t s);
 
 // Device-side per-row int8 quantisation.
 int launch_quantize_w8(const uint16_t* w, int64_t ldw, int8_t* q, int64_t ldq,

@@ -207,14 +207,19 @@ int launch_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 }  // namespace
 
 // bf16 calls that meet gemm_kernel's requirements run there (direct-to-LDS
-// loads, XCD-aware order) — except up to kSplitkMaxM rows against at most 8192
-// weight rows (Qwen3 QKV: 6144), which give too few 256-row tiles for 256 CUs
-// and run the split-K tiles; int8, unaligned rows and K tails run
-// tiled_kernel.
+// loads, XCD-aware order): split across workgroups when the plan says so and
+// the caller gave a workspace, else unsplit — except, without the split, up
+// to kSplitkMaxM rows against at most 8192 weight rows with K >=
+// kSplitkMinKTiled (Qwen3-4B QKV: 6144 x 2560), which give too few tiles for
+// 256 CUs and run the in-workgroup split-K tiles. int8, unaligned rows and K
+// tails run tiled_kernel.
 template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
-  if (!W8 && a.M <= kSplitkMaxM && wrows <= kSplitkSmallN && splitk_supported(a, aligned))
+  GemmSplit sp;
+  if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP>(a, sp, s);
+  if (!W8 && a.M <= kSplitkMaxM && wrows <= kSplitkSmallN && a.K >= kSplitkMinKTiled &&
+      splitk_supported(a, aligned))
     return launch_splitk<GATEUP>(a, s);
   if (!W8 && gemm_supported(a, aligned)) return launch_gemm<GATEUP>(a, s);
   return launch_cfg<128, 128, 64, 2, 2, GATEUP, W8>(a, aligned, s);

@@ -1,5 +1,6 @@
 // torch_ops.cpp — the thin PyTorch-ROCm custom ops over the C ABI of
-// include/llms_amd_fp.h. Each op allocates its output with torch on the
+// include/llms_amd_fp.h. Each op allocates its output (and, for the bf16
+// calls that split k across workgroups, the workspace) with torch on the
 // tensor's device, takes torch's current HIP stream, and hands plain pointers,
 // row strides and sizes to the C ABI; a nonzero fp_status becomes a
 // c10::Error (RuntimeError in Python). No computation happens here.
@@ -28,15 +29,24 @@ void* cur_stream(const at::Tensor& t) {
   return (void*)c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
 
+// Split-k workspace for a bf16 call, from torch's caching allocator on the
+// current stream (empty when the call does not split).
+at::Tensor workspace(const at::Tensor& x, int64_t M, int64_t N, int64_t K, bool gate_up) {
+  const int64_t bytes = fp_workspace_bytes(M, N, K, gate_up ? 1 : 0);
+  return at::empty({bytes}, x.options().dtype(at::kByte));
+}
+
 at::Tensor qkv(const at::Tensor& x, const at::Tensor& w, int64_t n_q, int64_t n_k) {
   check_2d(x, "x", at::kBFloat16);
   check_2d(w, "W_qkv", at::kBFloat16);
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
-  check_status(fp_qkv_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
-                           y.stride(0), M, n_q, n_k, K, cur_stream(x)),
-               "fp_qkv_bf16");
+  at::Tensor ws = workspace(x, M, N, K, false);
+  check_status(fp_qkv_bf16_ws(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
+                              y.stride(0), M, n_q, n_k, K, ws.numel() ? ws.data_ptr() : nullptr,
+                              ws.numel(), cur_stream(x)),
+               "fp_qkv_bf16_ws");
   return y;
 }
 
@@ -47,10 +57,12 @@ at::Tensor gate_up_silu(const at::Tensor& x, const at::Tensor& wg, const at::Ten
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = wg.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
-  check_status(fp_gate_up_silu_bf16(x.data_ptr(), x.stride(0), wg.data_ptr(), wg.stride(0),
-                                    wu.data_ptr(), wu.stride(0), y.data_ptr(), y.stride(0), M, N,
-                                    K, cur_stream(x)),
-               "fp_gate_up_silu_bf16");
+  at::Tensor ws = workspace(x, M, N, K, true);
+  check_status(fp_gate_up_silu_bf16_ws(x.data_ptr(), x.stride(0), wg.data_ptr(), wg.stride(0),
+                                       wu.data_ptr(), wu.stride(0), y.data_ptr(), y.stride(0), M,
+                                       N, K, ws.numel() ? ws.data_ptr() : nullptr, ws.numel(),
+                                       cur_stream(x)),
+               "fp_gate_up_silu_bf16_ws");
   return y;
 }
 
@@ -98,9 +110,11 @@ at::Tensor linear(const at::Tensor& x, const at::Tensor& w) {
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
-  check_status(fp_linear_bf16(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(),
-                              y.stride(0), M, N, K, cur_stream(x)),
-               "fp_linear_bf16");
+  at::Tensor ws = workspace(x, M, N, K, false);
+  check_status(fp_linear_bf16_ws(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                                 y.data_ptr(), y.stride(0), M, N, K,
+                                 ws.numel() ? ws.data_ptr() : nullptr, ws.numel(), cur_stream(x)),
+               "fp_linear_bf16_ws");
   return y;
 }
 

@@ -32,7 +32,8 @@ def test_header_declares_entry_points():
     names = _declared_functions()
     for expected in ("fp_qkv_bf16", "fp_gate_up_silu_bf16", "fp_qkv_w8",
                      "fp_gate_up_silu_w8", "fp_quantize_w8_per_row",
-                     "fp_linear_bf16", "fp_linear_w8",
+                     "fp_linear_bf16", "fp_linear_w8", "fp_workspace_bytes",
+                     "fp_qkv_bf16_ws", "fp_gate_up_silu_bf16_ws", "fp_linear_bf16_ws",
                      "fp_status_string", "fp_abi_version"):
         assert expected in names
 
@@ -45,6 +46,39 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in include/ but not exported"
         assert name in _lib.CAPI_SIGNATURES, f"{name} has no ctypes signature"
     assert lib.fp_abi_version() >> 16 == 1
+
+
+def test_workspace_bytes_plan():
+    """The split-k plan (a host function: no GPU needed). Splits only where
+    the unsplit grid leaves the chip idle and k is long: Qwen3 down/o from 32
+    rows, 4B QKV at 256 rows; never for short K, few rows, K % 64 != 0 or a
+    chip-filling grid. The workspace holds one fp32 plane per k range, 2..16
+    ranges, of M x N (gate-up: M x 2N)."""
+    from llms_amd import _lib
+
+    wb = _lib.capi().fp_workspace_bytes
+
+    def planes(M, N, K, gu=0):
+        b = wb(M, N, K, gu)
+        plane = 4 * M * N * (2 if gu else 1)
+        assert b % plane == 0
+        return b // plane
+
+    for M in (32, 64, 128, 256, 512, 1024):
+        assert 2 <= planes(M, 2560, 9728) <= 16, M          # 4B down
+        assert 2 <= planes(M, 4096, 12288) <= 16, M         # 8B down
+    assert 2 <= planes(256, 6144, 2560) <= 16               # 4B QKV, 256 rows
+    assert 2 <= planes(300, 1001, 8192) <= 16                # narrow, ragged N
+    assert 2 <= planes(64, 12288, 4096, 1) <= 16             # 8B gate-up, 64 rows
+    assert 2 <= planes(200, 1001, 8192, 1) <= 16             # gate-up, ragged N
+    for args in [(16, 2560, 9728, 0), (31, 2560, 9728, 0), (512, 6144, 2560, 0),
+                 (2048, 9728, 2560, 1), (256, 4096, 1024, 0), (64, 2560, 4096, 0),
+                 (512, 2560, 9736, 0), (8192, 2560, 9728, 0), (0, 2560, 9728, 0),
+                 (512, 0, 9728, 0), (64, 9728, 2560, 1), (32, 12288, 4096, 1),
+                 (128, 9728, 2560, 1), (32, 6144, 4096, 0)]:
+        assert wb(*args) == 0, args
+    # ranges hold at least 8 k-steps of 64
+    assert planes(32, 2560, 2048) <= 4
 
 
 def test_status_strings():
@@ -85,6 +119,13 @@ def test_argument_errors_return_before_launch():
     assert lib.fp_linear_bf16(P, 64, None, 64, P, 32, 2, 32, 64, None) == 1  # NULL w
     assert lib.fp_linear_w8(P, 64, P, 64, None, P, 32, 2, 32, 64, None) == 1  # NULL scale
     assert lib.fp_linear_w8(P, 64, P, 63, P, P, 32, 2, 32, 64, None) == 3    # ldq < K
+    # workspace variants: negative size or a misaligned workspace
+    assert lib.fp_linear_bf16_ws(P, 64, P, 64, P, 32, 2, 32, 64, P, -4, None) == 6
+    assert lib.fp_linear_bf16_ws(P, 64, P, 64, P, 32, 2, 32, 64, ctypes.c_void_p(20), 64, None) == 6
+    assert lib.fp_qkv_bf16_ws(P, 64, P, 64, P, 96, 2, 64, 16, 64, ctypes.c_void_p(8), 64, None) == 6
+    assert lib.fp_gate_up_silu_bf16_ws(P, 64, P, 64, P, 64, P, 32, 2, 32, 64, P, -1, None) == 6
+    assert lib.fp_qkv_bf16_ws(P, 64, P, 64, P, 96, 2, 0, 16, 64, None, 0, None) == 2
+    assert lib.fp_linear_bf16_ws(None, 64, None, 64, None, 32, 0, 32, 64, None, 0, None) == 0
     assert lib.fp_quantize_w8_per_row(P, 64, P, 63, P, 8, 64, None) == 3
     assert lib.fp_quantize_w8_per_row(P, 64, P, 64, P, -1, 64, None) == 2
     assert lib.fp_quantize_w8_per_row(None, 64, None, 64, None, 0, 64, None) == 0
@@ -165,6 +206,30 @@ def test_capi_raw_pointers_match_oracle():
     torch.cuda.synchronize()
     p = ref.check_parity(bits(y), ref.ref_gate_up_silu_full(bits(x), bits(wg), bits(wu)))
     assert p.ok, p
+
+    # the workspace variant: split k (planned for this shape) and unsplit
+    # (workspace one float short) both match the oracle; the unsplit call is
+    # bit-identical to the plain entry point
+    Mw, Kw, Nw = 512, 9728, 2560
+    xw, ww = qkv_inputs(92, Mw, Kw, Nw, 0)
+    xwd, wwd = xw.cuda(), ww.cuda()
+    need = lib.fp_workspace_bytes(Mw, Nw, Kw, 0)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    y_split = torch.empty(Mw, Nw, dtype=torch.bfloat16, device="cuda")
+    y_short = torch.empty_like(y_split)
+    y_plain = torch.empty_like(y_split)
+    assert lib.fp_linear_bf16_ws(_p(xwd), Kw, _p(wwd), Kw, _p(y_split), Nw, Mw, Nw, Kw, _p(ws),
+                                 need, stream) == 0
+    assert lib.fp_linear_bf16_ws(_p(xwd), Kw, _p(wwd), Kw, _p(y_short), Nw, Mw, Nw, Kw, _p(ws),
+                                 need - 4, stream) == 0
+    assert lib.fp_linear_bf16(_p(xwd), Kw, _p(wwd), Kw, _p(y_plain), Nw, Mw, Nw, Kw, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y_short.view(torch.int16), y_plain.view(torch.int16))
+    rows = np.arange(0, Mw, 5)
+    for y_ in (y_split, y_plain):
+        p = ref.check_parity(bits(y_)[rows], ref.ref_linear(bits(xw)[rows], bits(ww)))
+        assert p.ok, p
 
     # int8 through the raw ABI: quantise on device, then the fused call
     q = torch.empty(I, K, dtype=torch.int8, device="cuda")

@@ -407,6 +407,39 @@ def test_linear_tails(M, K, N):
     check_linear(120 + M, M, K, N)
 
 
+@pytest.mark.parametrize("M,N,K,op", [
+    (32, 2560, 9728, "linear"), (100, 4096, 12288, "linear"), (300, 1001, 8192, "linear"),
+    (1024, 2560, 9728, "linear"), (2048, 1024, 3072, "linear"), (256, 6144, 2560, "qkv"),
+    (64, 12288, 4096, "gate-up"), (200, 1001, 8192, "gate-up"), (77, 4096, 4096, "linear")])
+def test_split_k_across_workgroups(M, N, K, op):
+    """Calls the planner splits across workgroups (fp32 partials in a torch
+    workspace, fixed-order reduce): narrow and ragged N (scalar partial
+    stores), ragged M, every split tile; repeated calls are bit-identical."""
+    from llms_amd import _lib
+
+    assert _lib.capi().fp_workspace_bytes(M, N, K, int(op == "gate-up")) > 0
+    kern = _kernels()
+    if op == "gate-up":
+        x, wg, wu = ffn_inputs(150 + M, M, K, N)
+        xd, gd, ud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+        y = kern.triton_fused_gate_up_silu(xd, gd, ud)
+        assert torch.equal(y.view(torch.int16), kern.triton_fused_gate_up_silu(xd, gd, ud).view(torch.int16))
+        rows = _rows(M, limit=96)
+        _check(y.cpu()[rows], ref.ref_gate_up_silu_full(bits(x)[rows], bits(wg), bits(wu)), f"split gate-up M={M} N={N} K={K}")
+        return
+    x, w = qkv_inputs(160 + M, M, K, N, 0)
+    xd, wd = x.to(DEV), w.to(DEV)
+    if op == "qkv":
+        n_k = N // 6
+        run = lambda: torch.cat(kern.triton_fused_qkv(xd, wd, n_q=N - 2 * n_k, n_k=n_k), dim=-1)  # noqa: E731
+    else:
+        run = lambda: kern.fused_linear(xd, wd)  # noqa: E731
+    y = run()
+    assert torch.equal(y.view(torch.int16), run().view(torch.int16))
+    rows = _rows(M, limit=96)
+    _check(y.cpu()[rows], ref.ref_linear(bits(x)[rows], bits(w)), f"split {op} M={M} N={N} K={K}")
+
+
 @pytest.mark.parametrize("M", [1, 4, 64, 2048])
 def test_linear_int8(M):
     K, N = 9728, 2560
