@@ -395,12 +395,18 @@ int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
 // they fill the chip, smaller tiles (2 per CU) win where they save a round.
 // QKV-sized outputs (<= 8192 weight rows): 64 x 128 tiles with three stages
 // to 768 rows, 128 x 128 to 1536, then 256 x 256. Outputs of at most 4096
-// columns (the down and o projections) keep 128 x 128 to 4096 rows: a 256 x
-// 256 grid there is under one round (2048 x 2560 -> 80 tiles). Gate-up-sized:
+// columns (the down and o projections) keep 128 x 128 until a 256 x 256 grid
+// fills the chip (2048 x 2560 -> 80 tiles: 128 x 128; 4096 x 4096 -> 256
+// tiles: 256 x 256). Gate-up-sized:
 // 128 x 128 to 384 rows, 256 x 256 to 768 (152-192 tiles, one round), 128 x
 // 128 to 1536, 256 x 256.
 int gemm_tile_unsplit(int64_t M, int64_t wrows) {
-  if (wrows <= 4096) return M <= 768 ? kT64x128 : (M <= 4096 ? kT128x128 : kT256x256);
+  if (wrows <= 4096) {
+    if (M <= 768) return kT64x128;
+    // 256 x 256 once its grid fills the chip (8B down, 4096 x 4096: 256 tiles)
+    if (tile_count(kT256x256, M, wrows, false) >= kCUs) return kT256x256;
+    return kT128x128;
+  }
   if (wrows <= 8192) return M <= 768 ? kT64x128 : (M <= 1536 ? kT128x128 : kT256x256);
   if (M <= 384) return kT128x128;
   if (M <= 768) return kT256x256;

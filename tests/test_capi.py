@@ -231,6 +231,29 @@ def test_capi_raw_pointers_match_oracle():
         p = ref.check_parity(bits(y_)[rows], ref.ref_linear(bits(xw)[rows], bits(ww)))
         assert p.ok, p
 
+    # the other workspace variants with the planned workspace (QKV at 256
+    # rows splits; gate-up here does not, so its workspace is unused)
+    Mq, nq, nk, Kq = 256, 4096, 1024, 2560
+    xq, wq = qkv_inputs(93, Mq, Kq, nq, nk)
+    xqd, wqd = xq.cuda(), wq.cuda()
+    Nq = nq + 2 * nk
+    need = lib.fp_workspace_bytes(Mq, Nq, Kq, 0)
+    assert need > 0
+    wsq = torch.empty(need, dtype=torch.uint8, device="cuda")
+    yq = torch.empty(Mq, Nq, dtype=torch.bfloat16, device="cuda")
+    assert lib.fp_qkv_bf16_ws(_p(xqd), Kq, _p(wqd), Kq, _p(yq), Nq, Mq, nq, nk, Kq, _p(wsq), need,
+                              stream) == 0
+    torch.cuda.synchronize()
+    rows = np.arange(0, Mq, 3)
+    p = ref.check_parity(bits(yq)[rows], ref.ref_qkv_full(bits(xq)[rows], bits(wq), nq, nk))
+    assert p.ok, p
+    yg = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    assert lib.fp_gate_up_silu_bf16_ws(_p(xd), K, _p(gd), K, _p(ud), K, _p(yg), I, M, I, K,
+                                       _p(wsq), need, stream) == 0
+    torch.cuda.synchronize()
+    p = ref.check_parity(bits(yg), ref.ref_gate_up_silu_full(bits(x), bits(wg), bits(wu)))
+    assert p.ok, p
+
     # int8 through the raw ABI: quantise on device, then the fused call
     q = torch.empty(I, K, dtype=torch.int8, device="cuda")
     s = torch.empty(I, dtype=torch.float32, device="cuda")
@@ -246,3 +269,15 @@ def test_capi_raw_pointers_match_oracle():
                                        q2.cpu().numpy(), s2.cpu().numpy())
     p = ref.check_parity(bits(y), out)
     assert p.ok, p
+
+    # int8 QKV-shaped and plain projections on the same quantised Wg (I rows)
+    y8 = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    assert lib.fp_qkv_w8(_p(xd), K, _p(q), K, _p(s), _p(y8), I, M, I - 2 * 1024, 1024, K,
+                         stream) == 0
+    y9 = torch.empty_like(y8)
+    assert lib.fp_linear_w8(_p(xd), K, _p(q), K, _p(s), _p(y9), I, M, I, K, stream) == 0
+    torch.cuda.synchronize()
+    out = ref.ref_linear_w8(bits(x), q.cpu().numpy(), s.cpu().numpy())
+    for yy in (y8, y9):
+        p = ref.check_parity(bits(yy), out)
+        assert p.ok, p
