@@ -236,6 +236,27 @@ def counters_run(torch, kern, shape, layers: int) -> dict:
     }
 
 
+def linear_run(torch, kern, M: int, N: int, K: int, reps: int) -> dict:
+    """The plain projection y = x W^T (the engine's down / o Linears) over
+    weight sets cycled past the Infinity Cache: average launch duration by
+    graph replay, and torch's F.linear (hipBLASLt) on the same shape for scale."""
+    import torch.nn.functional as F
+
+    sets = max(2, min(32, (600 << 20) // (2 * N * K)))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    ws = [(torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+          for _ in range(sets)]
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    ours = kernel_seconds(torch, [lambda w=w: kern.fused_linear(x, w) for w in ws], reps)
+    ref = kernel_seconds(torch, [lambda w=w: F.linear(x, w) for w in ws], reps)
+    flops = 2 * M * N * K
+    return {"mode": "linear", "M": M, "N": N, "K": K, "weight_sets": sets,
+            "us": round(ours * 1e6, 2), "tflops": round(flops / ours / 1e12, 1),
+            "gbs": round((2 * N * K + 2 * M * K + 2 * M * N) / ours / 1e9, 1),
+            "hipblaslt_us": round(ref * 1e6, 2)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,6 +271,9 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--counters", action="store_true",
                     help="run only the short fixed sequence used for rocprofv3 --pmc runs")
+    ap.add_argument("--linear", metavar="M,N,K",
+                    help="time only the plain projection (down / o) of this shape over "
+                         "cycled weight sets and print one JSON line (profiling aid)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -274,6 +298,10 @@ def main() -> int:
     L = args.layers
     if args.counters:
         print(json.dumps(counters_run(torch, kern, shape, L)), flush=True)
+        return 0
+    if args.linear:
+        M, N, Kl = (int(v) for v in args.linear.split(","))
+        print(json.dumps(linear_run(torch, kern, M, N, Kl, args.steps)), flush=True)
         return 0
 
     # ---------------- decode, M = 1: the headline ----------------
