@@ -51,7 +51,8 @@ typedef enum fp_status {
   FP_ERR_STRIDE = 3,     /* a row stride is smaller than the row length */
   FP_ERR_LAUNCH = 4,     /* the HIP launch reported an error */
   FP_ERR_DEVICE = 5,     /* no usable gfx950 device for the current context */
-  FP_ERR_WORKSPACE = 6   /* workspace not 16-byte aligned, or a negative size */
+  FP_ERR_WORKSPACE = 6   /* workspace missing or too small where required, not 16-byte
+                            aligned, or a negative size */
 } fp_status;
 
 /* Human-readable text for an fp_status value (static storage). */
@@ -164,6 +165,52 @@ int fp_linear_bf16_ws(const void* x, int64_t ldx,
                       int64_t M, int64_t N, int64_t K,
                       void* workspace, int64_t workspace_bytes,
                       void* stream);
+
+/*
+ * RMSNorm prologue fused with the projections (no reference counterpart as a
+ * kernel: it replaces the eager pair norm1(x) -> attention q/k/v and
+ * norm2(h) -> FFN gate/up, reference src/engine/model.py:57-66 with RMSNorm
+ * src/engine/attention.py:28-33). With gamma [K] bf16 and eps:
+ *   r     = 1 / sqrt(sum_k x[k]^2 / K + eps)            (fp32)
+ *   xn[k] = bf16(gamma[k] * bf16(x[k] * r))
+ * and then the contract of the matching projection on xn. Decode-sized calls
+ * (the row-streaming regime: bf16 M <= 2, int8 M <= 4, with room for x in
+ * LDS) run as one launch that normalises x while staging it; the others need
+ * fp_rmsnorm_workspace_bytes(M, N, K, gate_up, int8) bytes of workspace
+ * (the normalised rows, then any split-k partials) and return
+ * FP_ERR_WORKSPACE without it. eps must be finite and >= 0.
+ */
+int64_t fp_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up, int int8);
+
+int fp_rmsnorm_qkv_bf16(const void* x, int64_t ldx, const void* gamma, float eps,
+                        const void* w, int64_t ldw,
+                        void* y, int64_t ldy,
+                        int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+                        void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
+int fp_rmsnorm_gate_up_silu_bf16(const void* x, int64_t ldx, const void* gamma, float eps,
+                                 const void* wg, int64_t ldwg,
+                                 const void* wu, int64_t ldwu,
+                                 void* y, int64_t ldy,
+                                 int64_t M, int64_t N, int64_t K,
+                                 void* workspace, int64_t workspace_bytes,
+                                 void* stream);
+
+int fp_rmsnorm_qkv_w8(const void* x, int64_t ldx, const void* gamma, float eps,
+                      const int8_t* q, int64_t ldq, const float* scale,
+                      void* y, int64_t ldy,
+                      int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+                      void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
+int fp_rmsnorm_gate_up_silu_w8(const void* x, int64_t ldx, const void* gamma, float eps,
+                               const int8_t* qg, int64_t ldqg, const float* sg,
+                               const int8_t* qu, int64_t ldqu, const float* su,
+                               void* y, int64_t ldy,
+                               int64_t M, int64_t N, int64_t K,
+                               void* workspace, int64_t workspace_bytes,
+                               void* stream);
 
 /*
  * Per-output-channel symmetric int8 quantisation on the device (the packing

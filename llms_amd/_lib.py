@@ -28,7 +28,7 @@ class NativeLibraryMissing(RuntimeError):
 
 
 # (name, argtypes) of every entry point declared in include/llms_amd_fp.h.
-_P, _I64 = ctypes.c_void_p, ctypes.c_int64
+_P, _I64, _F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float
 CAPI_SIGNATURES: dict[str, list] = {
     "fp_status_string": [ctypes.c_int],
     "fp_abi_version": [],
@@ -43,6 +43,13 @@ CAPI_SIGNATURES: dict[str, list] = {
     "fp_qkv_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "fp_gate_up_silu_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "fp_linear_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "fp_rmsnorm_workspace_bytes": [_I64, _I64, _I64, ctypes.c_int, ctypes.c_int],
+    "fp_rmsnorm_qkv_bf16": [_P, _I64, _P, _F, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "fp_rmsnorm_gate_up_silu_bf16": [_P, _I64, _P, _F, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64,
+                                     _P, _I64, _P],
+    "fp_rmsnorm_qkv_w8": [_P, _I64, _P, _F, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "fp_rmsnorm_gate_up_silu_w8": [_P, _I64, _P, _F, _P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64,
+                                   _I64, _P, _I64, _P],
 }
 
 FP_STATUS = {
@@ -75,7 +82,8 @@ def capi() -> ctypes.CDLL:
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
                 fn.restype = {"fp_status_string": ctypes.c_char_p,
-                              "fp_workspace_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
+                              "fp_workspace_bytes": ctypes.c_int64,
+                              "fp_rmsnorm_workspace_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
             _capi = lib
         return _capi
 

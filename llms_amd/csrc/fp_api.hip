@@ -52,6 +52,40 @@ int run(const StreamArgs& a, bool aligned, hipStream_t s) {
   return launch_status(rc);
 }
 
+inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// RMSNorm prologue + projection: one launch on the rows kernel (x normalised
+// while it is staged in LDS), else the norm into the workspace and the plain
+// dispatch on the normalised rows (any split workspace follows them).
+// xaligned: x rows and K fit the vector path; waligned: the weights do.
+template <bool GATEUP, bool W8>
+int run_norm(StreamArgs a, bool xaligned, bool waligned, void* ws, int64_t ws_bytes,
+             hipStream_t s) {
+  if (a.M == 0) return FP_OK;
+  const bool galigned = al16(a.gamma);
+  if (rows_supported<W8>(a, xaligned && waligned && galigned))
+    return launch_status(launch_rows<GATEUP, W8>(a, s));
+  const int64_t xn_bytes = round_up(a.M * a.K * 2, 256);
+  if (!ws || ws_bytes < xn_bytes) return FP_ERR_WORKSPACE;
+  uint16_t* xn = (uint16_t*)ws;
+  int rc = launch_rmsnorm(a.x, a.ldx, a.gamma, a.eps, xn, a.M, a.K,
+                          xaligned && galigned && a.K % 8 == 0, s);
+  if (rc) return launch_status(rc);
+  StreamArgs b = a;
+  b.x = xn;
+  b.ldx = a.K;
+  b.gamma = nullptr;
+  b.ws = W8 ? nullptr : (float*)((char*)ws + xn_bytes);
+  b.ws_floats = W8 ? 0 : (ws_bytes - xn_bytes) / 4;
+  return run<GATEUP, W8>(b, waligned && a.K % (W8 ? 16 : 8) == 0, s);
+}
+
+int check_norm(float eps, void* ws, int64_t ws_bytes) {
+  if (!(eps >= 0.f) || eps > 3.0e38f) return FP_ERR_SHAPE;
+  if (ws_bytes < 0 || (ws && !al16(ws))) return FP_ERR_WORKSPACE;
+  return FP_OK;
+}
+
 int check_common(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
   if (M < 0 || N < 1 || K < 1) return FP_ERR_SHAPE;
   // grid.x = ceil(N / 16) must fit a 32-bit grid dimension; M tiles likewise.
@@ -75,12 +109,12 @@ const char* fp_status_string(int status) {
     case FP_ERR_STRIDE: return "row stride smaller than the row length";
     case FP_ERR_LAUNCH: return "HIP kernel launch failed";
     case FP_ERR_DEVICE: return "no gfx950 code object for the current device";
-    case FP_ERR_WORKSPACE: return "workspace not 16-byte aligned, or a negative workspace size";
+    case FP_ERR_WORKSPACE: return "workspace missing, too small or not 16-byte aligned, or a negative workspace size";
     default: return "unknown fp_status";
   }
 }
 
-int fp_abi_version(void) { return (1 << 16) | 2; }
+int fp_abi_version(void) { return (1 << 16) | 3; }
 
 int64_t fp_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up) {
   if (M < 1 || N < 1 || K < 1) return 0;
@@ -181,6 +215,88 @@ int fp_linear_bf16_ws(const void* x, int64_t ldx, const void* w, int64_t ldw, vo
 int fp_linear_w8(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,
                  void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
   return fp_qkv_w8(x, ldx, q, ldq, scale, y, ldy, M, N, 0, K, stream);
+}
+
+int64_t fp_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up, int int8) {
+  if (M < 1 || N < 1 || K < 1) return 0;
+  const bool w8 = int8 != 0;
+  if (M <= (w8 ? fp::kRowsMaxM : 2) && K % (w8 ? 16 : 8) == 0 && fp::rows_fit(M, K, w8)) return 0;
+  int64_t b = fp::round_up(M * K * 2, 256);
+  if (!w8) b += 4 * fp::gemm_split_ws_floats(fp::gemm_split_plan(M, N, K, gate_up != 0), M, N, K,
+                                             gate_up != 0);
+  return b;
+}
+
+int fp_rmsnorm_qkv_bf16(const void* x, int64_t ldx, const void* gamma, float eps, const void* w,
+                        int64_t ldw, void* y, int64_t ldy, int64_t M, int64_t n_q, int64_t n_k,
+                        int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (n_q < 1 || n_k < 0) return FP_ERR_SHAPE;
+  const int64_t N = n_q + 2 * n_k;
+  int st = fp::check_common(M, N, K, ldx, ldy);
+  if (st) return st;
+  if (ldw < K) return FP_ERR_STRIDE;
+  if ((st = fp::check_norm(eps, workspace, workspace_bytes))) return st;
+  if (M == 0) return FP_OK;
+  if (!x || !gamma || !w || !y) return FP_ERR_NULL;
+  StreamArgs a{(const uint16_t*)x, ldx, w, ldw, nullptr, 0, nullptr, nullptr, (uint16_t*)y, ldy,
+               M, N, K, nullptr, 0, (const uint16_t*)gamma, eps};
+  const bool xal = K % 8 == 0 && ldx % 8 == 0 && fp::al16(x);
+  const bool wal = ldw % 8 == 0 && fp::al16(w);
+  return fp::run_norm<false, false>(a, xal, wal, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int fp_rmsnorm_gate_up_silu_bf16(const void* x, int64_t ldx, const void* gamma, float eps,
+                                 const void* wg, int64_t ldwg, const void* wu, int64_t ldwu,
+                                 void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  int st = fp::check_common(M, N, K, ldx, ldy);
+  if (st) return st;
+  if (ldwg < K || ldwu < K) return FP_ERR_STRIDE;
+  if ((st = fp::check_norm(eps, workspace, workspace_bytes))) return st;
+  if (M == 0) return FP_OK;
+  if (!x || !gamma || !wg || !wu || !y) return FP_ERR_NULL;
+  StreamArgs a{(const uint16_t*)x, ldx, wg, ldwg, wu, ldwu, nullptr, nullptr, (uint16_t*)y, ldy,
+               M, N, K, nullptr, 0, (const uint16_t*)gamma, eps};
+  const bool xal = K % 8 == 0 && ldx % 8 == 0 && fp::al16(x);
+  const bool wal = ldwg % 8 == 0 && ldwu % 8 == 0 && fp::al16(wg) && fp::al16(wu);
+  return fp::run_norm<true, false>(a, xal, wal, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int fp_rmsnorm_qkv_w8(const void* x, int64_t ldx, const void* gamma, float eps, const int8_t* q,
+                      int64_t ldq, const float* scale, void* y, int64_t ldy, int64_t M,
+                      int64_t n_q, int64_t n_k, int64_t K, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
+  if (n_q < 1 || n_k < 0) return FP_ERR_SHAPE;
+  const int64_t N = n_q + 2 * n_k;
+  int st = fp::check_common(M, N, K, ldx, ldy);
+  if (st) return st;
+  if (ldq < K) return FP_ERR_STRIDE;
+  if ((st = fp::check_norm(eps, workspace, workspace_bytes))) return st;
+  if (M == 0) return FP_OK;
+  if (!x || !gamma || !q || !scale || !y) return FP_ERR_NULL;
+  StreamArgs a{(const uint16_t*)x, ldx, q, ldq, nullptr, 0, scale, nullptr, (uint16_t*)y, ldy,
+               M, N, K, nullptr, 0, (const uint16_t*)gamma, eps};
+  const bool xal = K % 16 == 0 && ldx % 8 == 0 && fp::al16(x);
+  const bool wal = ldq % 16 == 0 && fp::al16(q);
+  return fp::run_norm<false, true>(a, xal, wal, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int fp_rmsnorm_gate_up_silu_w8(const void* x, int64_t ldx, const void* gamma, float eps,
+                               const int8_t* qg, int64_t ldqg, const float* sg, const int8_t* qu,
+                               int64_t ldqu, const float* su, void* y, int64_t ldy, int64_t M,
+                               int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                               void* stream) {
+  int st = fp::check_common(M, N, K, ldx, ldy);
+  if (st) return st;
+  if (ldqg < K || ldqu < K) return FP_ERR_STRIDE;
+  if ((st = fp::check_norm(eps, workspace, workspace_bytes))) return st;
+  if (M == 0) return FP_OK;
+  if (!x || !gamma || !qg || !sg || !qu || !su || !y) return FP_ERR_NULL;
+  StreamArgs a{(const uint16_t*)x, ldx, qg, ldqg, qu, ldqu, sg, su, (uint16_t*)y, ldy,
+               M, N, K, nullptr, 0, (const uint16_t*)gamma, eps};
+  const bool xal = K % 16 == 0 && ldx % 8 == 0 && fp::al16(x);
+  const bool wal = ldqg % 16 == 0 && ldqu % 16 == 0 && fp::al16(qg) && fp::al16(qu);
+  return fp::run_norm<true, true>(a, xal, wal, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int fp_quantize_w8_per_row(const void* w, int64_t ldw, int8_t* q, int64_t ldq, float* scale,

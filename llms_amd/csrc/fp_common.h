@@ -37,6 +37,25 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
+// ---- wave reduction -------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave (wave-uniform result), fixed order.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror: sums of 8
+  v += dpp_f32<0x140>(v);  // row_mirror: sums of 16
+  return (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16))) +
+         (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48)));
+}
+
 // ---- epilogues -------------------------------------------------------------
 
 // silu(g) * u with the rounding points of the unfused bf16 torch path:

@@ -26,6 +26,9 @@ struct StreamArgs {
   // (16-byte aligned; NULL / too small: the unsplit kernels run).
   float* ws;
   int64_t ws_floats;
+  // Optional RMSNorm prologue of x (fp_norm.h): weight [K] bf16 and eps.
+  const uint16_t* gamma;
+  float eps;
 };
 
 // Weight-streaming kernels (M <= 64). Return the launch's hipError_t.
@@ -40,8 +43,17 @@ constexpr int64_t kRowsMaxM = 4;
 constexpr int64_t kRowsMaxLds = 65536;
 template <bool W8>
 bool rows_supported(const StreamArgs& a, bool aligned);
+// With a.gamma set, the rows kernel normalises x while staging it (one
+// launch for the RMSNorm prologue and the projection).
 template <bool GATEUP, bool W8>
 int launch_rows(const StreamArgs& a, hipStream_t s);
+// Whether M x K fits the rows kernel's x staging (shape only; alignment and
+// the M limit of rows_supported apply on top).
+bool rows_fit(int64_t M, int64_t K, bool w8);
+
+// RMSNorm prologue on its own (fp_norm.h): xn [M, K] (row stride K) from x.
+int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* gamma, float eps,
+                   uint16_t* xn, int64_t M, int64_t K, bool vec, hipStream_t s);
 
 // LDS-tiled MFMA kernels (M > 64). Return the launch's hipError_t.
 template <bool GATEUP, bool W8>

@@ -30,6 +30,7 @@
 // rows with K % 8 == 0 (int8: K % 16 == 0), staged x within kRowsMaxLds.
 #include "fp_common.h"
 #include "fp_launch.h"
+#include "fp_norm.h"
 
 namespace fp {
 
@@ -38,23 +39,6 @@ namespace {
 // k elements per wave instruction (64 lanes x 16 B)
 template <bool W8>
 constexpr int kc() { return W8 ? 1024 : 512; }
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-// Sum over the 64 lanes of a wave (wave-uniform result), fixed order.
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp_f32<0xb1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_f32<0x4e>(v);   // quad_perm [2,3,0,1]
-  v += dpp_f32<0x141>(v);  // row_half_mirror: sums of 8
-  v += dpp_f32<0x140>(v);  // row_mirror: sums of 16
-  return (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
-          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16))) +
-         (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
-          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48)));
-}
 
 typedef __attribute__((ext_vector_type(2))) float f32x2;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
@@ -87,8 +71,9 @@ __device__ __forceinline__ float diag(f32x4 d, int lane) {
 }
 
 // NW waves per workgroup, R rows per wave, U weight chunks in flight per wave,
-// MM x rows (the call's M rounded up; the extra rows are zeros in LDS).
-template <int NW, int R, int U, int MM, bool GATEUP, bool W8>
+// MM x rows (the call's M rounded up; the extra rows are zeros in LDS). NORM:
+// x is RMS-normalised (a.gamma, a.eps) on its way into LDS.
+template <int NW, int R, int U, int MM, bool GATEUP, bool W8, bool NORM>
 __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   constexpr int KC = kc<W8>();
   constexpr int KL = KC / kWave;  // k elements per lane per chunk
@@ -125,10 +110,31 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   // x[0:MM, 0:K] -> LDS rows of Kp = J * KC, zero beyond K and beyond M
   const int64_t Kp = (int64_t)J * KC;
   const int64_t nvec = MM * (Kp / 8);
-  for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave) {
-    const int64_t m = i / (Kp / 8), k = (i - m * (Kp / 8)) * 8;
-    *reinterpret_cast<u32x4*>(xs + i * 8) =
-        m < a.M ? load_bf16x8<true>(a.x + m * a.ldx, k, K) : u32x4{0, 0, 0, 0};
+  if constexpr (NORM) {
+    // every workgroup computes the same per-row scales (fixed-order sums)
+    __shared__ float red[NW];
+    __shared__ float rinv[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      if (m < a.M) {
+        const float ss = row_sumsq<NW * kWave, true>(a.x + m * a.ldx, K, red);
+        if (threadIdx.x == 0) rinv[m] = rms_scale(ss, K, a.eps);
+      }
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave) {
+      const int64_t m = i / (Kp / 8), k = (i - m * (Kp / 8)) * 8;
+      *reinterpret_cast<u32x4*>(xs + i * 8) =
+          m < a.M ? norm_bf16x8(load_bf16x8<true>(a.x + m * a.ldx, k, K),
+                                load_bf16x8<true>(a.gamma, k, K), rinv[m])
+                  : u32x4{0, 0, 0, 0};
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave) {
+      const int64_t m = i / (Kp / 8), k = (i - m * (Kp / 8)) * 8;
+      *reinterpret_cast<u32x4*>(xs + i * 8) =
+          m < a.M ? load_bf16x8<true>(a.x + m * a.ldx, k, K) : u32x4{0, 0, 0, 0};
+    }
   }
   __syncthreads();
 
@@ -216,9 +222,29 @@ template <int NW, int R, int U, int MM, bool GATEUP, bool W8>
 int launch_rows_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t per = (int64_t)NW * R;
   const size_t shm = (size_t)rows_lds_bytes<W8>(MM, a.K);
-  hipLaunchKernelGGL((rows_kernel<NW, R, U, MM, GATEUP, W8>), dim3((unsigned)((a.N + per - 1) / per)),
-                     dim3(NW * kWave), shm, s, a);
+  const dim3 grid((unsigned)((a.N + per - 1) / per)), block(NW * kWave);
+  if (a.gamma)
+    hipLaunchKernelGGL((rows_kernel<NW, R, U, MM, GATEUP, W8, true>), grid, block, shm, s, a);
+  else
+    hipLaunchKernelGGL((rows_kernel<NW, R, U, MM, GATEUP, W8, false>), grid, block, shm, s, a);
   return (int)hipGetLastError();
+}
+
+// One workgroup per row: the row's scale, then the normalised row.
+template <bool VEC>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, int64_t ldx,
+                                                      const uint16_t* gamma, float eps,
+                                                      uint16_t* xn, int64_t K) {
+  __shared__ float red[256 / kWave];
+  const uint16_t* row = x + (int64_t)blockIdx.x * ldx;
+  uint16_t* out = xn + (int64_t)blockIdx.x * K;
+  const float r = rms_scale(row_sumsq<256, VEC>(row, K, red), K, eps);
+  if constexpr (VEC) {
+    for (int64_t k = (int64_t)threadIdx.x * 8; k < K; k += 256 * 8)
+      *reinterpret_cast<u32x4*>(out + k) = norm_bf16x8(ld16(row + k), ld16(gamma + k), r);
+  } else {
+    for (int64_t k = threadIdx.x; k < K; k += 256) out[k] = (uint16_t)norm_bf16(row[k], gamma[k], r);
+  }
 }
 
 }  // namespace
@@ -226,6 +252,21 @@ int launch_rows_cfg(const StreamArgs& a, hipStream_t s) {
 // bf16 takes M <= 2 here (for 3..4 rows the 8-row streaming kernel is
 // faster: its MFMA columns hold the x rows), int8 up to kRowsMaxM (the
 // dequantisation, shared by all x rows, dominates).
+bool rows_fit(int64_t M, int64_t K, bool w8) {
+  return (w8 ? rows_lds_bytes<true>(M, K) : rows_lds_bytes<false>(M, K)) <= kRowsMaxLds;
+}
+
+int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* gamma, float eps,
+                   uint16_t* xn, int64_t M, int64_t K, bool vec, hipStream_t s) {
+  if (vec)
+    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((unsigned)M), dim3(256), 0, s, x, ldx, gamma,
+                       eps, xn, K);
+  else
+    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, x, ldx, gamma,
+                       eps, xn, K);
+  return (int)hipGetLastError();
+}
+
 template <bool W8>
 bool rows_supported(const StreamArgs& a, bool aligned) {
   const int64_t max_m = W8 ? kRowsMaxM : 2;

@@ -134,6 +134,107 @@ at::Tensor linear_w8(const at::Tensor& x, const at::Tensor& q, const at::Tensor&
   return y;
 }
 
+// ---- RMSNorm prologue fused with the projections ----
+
+void check_gamma(const at::Tensor& gamma, int64_t K) {
+  TORCH_CHECK(gamma.dim() == 1 && gamma.scalar_type() == at::kBFloat16 && gamma.is_contiguous(),
+              "norm weight must be a contiguous 1-D bfloat16 tensor");
+  TORCH_CHECK(gamma.size(0) == K, "norm weight has ", gamma.size(0), " elements, x has K = ", K);
+  TORCH_CHECK(gamma.is_cuda(), "norm weight must be a HIP device tensor");
+}
+
+// Workspace for a fused-norm call: what the library asks for, and at least
+// room for the normalised rows (decode-sized calls whose pointers do not fit
+// the one-launch path fall back to it).
+at::Tensor norm_workspace(const at::Tensor& x, int64_t M, int64_t N, int64_t K, bool gate_up,
+                          bool int8) {
+  int64_t bytes = fp_rmsnorm_workspace_bytes(M, N, K, gate_up ? 1 : 0, int8 ? 1 : 0);
+  const int64_t rows = (M * K * 2 + 255) / 256 * 256;
+  return at::empty({bytes > rows ? bytes : rows}, x.options().dtype(at::kByte));
+}
+
+at::Tensor rmsnorm_qkv(const at::Tensor& x, const at::Tensor& gamma, double eps,
+                       const at::Tensor& w, int64_t n_q, int64_t n_k) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(w, "W_qkv", at::kBFloat16);
+  const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
+  check_gamma(gamma, K);
+  const c10::DeviceGuard guard(x.device());
+  at::Tensor y = at::empty({M, N}, x.options());
+  at::Tensor ws = norm_workspace(x, M, N, K, false, false);
+  check_status(fp_rmsnorm_qkv_bf16(x.data_ptr(), x.stride(0), gamma.data_ptr(), (float)eps,
+                                   w.data_ptr(), w.stride(0), y.data_ptr(), y.stride(0), M, n_q,
+                                   n_k, K, ws.data_ptr(), ws.numel(), cur_stream(x)),
+               "fp_rmsnorm_qkv_bf16");
+  return y;
+}
+
+at::Tensor rmsnorm_gate_up_silu(const at::Tensor& x, const at::Tensor& gamma, double eps,
+                                const at::Tensor& wg, const at::Tensor& wu) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(wg, "Wg", at::kBFloat16);
+  check_2d(wu, "Wu", at::kBFloat16);
+  const int64_t M = x.size(0), K = x.size(1), N = wg.size(0);
+  check_gamma(gamma, K);
+  const c10::DeviceGuard guard(x.device());
+  at::Tensor y = at::empty({M, N}, x.options());
+  at::Tensor ws = norm_workspace(x, M, N, K, true, false);
+  check_status(fp_rmsnorm_gate_up_silu_bf16(x.data_ptr(), x.stride(0), gamma.data_ptr(),
+                                            (float)eps, wg.data_ptr(), wg.stride(0),
+                                            wu.data_ptr(), wu.stride(0), y.data_ptr(),
+                                            y.stride(0), M, N, K, ws.data_ptr(), ws.numel(),
+                                            cur_stream(x)),
+               "fp_rmsnorm_gate_up_silu_bf16");
+  return y;
+}
+
+void check_scale(const at::Tensor& s, const at::Tensor& q, const char* name) {
+  TORCH_CHECK(s.dim() == 1 && s.scalar_type() == at::kFloat && s.is_contiguous(), name,
+              " must be a contiguous 1-D float32 tensor");
+  TORCH_CHECK(s.size(0) == q.size(0), name, " has ", s.size(0), " rows, q has ", q.size(0));
+}
+
+at::Tensor rmsnorm_qkv_w8(const at::Tensor& x, const at::Tensor& gamma, double eps,
+                          const at::Tensor& q, const at::Tensor& s, int64_t n_q, int64_t n_k) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(q, "q", at::kChar);
+  check_scale(s, q, "scale");
+  const int64_t M = x.size(0), K = x.size(1), N = q.size(0);
+  check_gamma(gamma, K);
+  const c10::DeviceGuard guard(x.device());
+  at::Tensor y = at::empty({M, N}, x.options());
+  at::Tensor ws = norm_workspace(x, M, N, K, false, true);
+  check_status(fp_rmsnorm_qkv_w8(x.data_ptr(), x.stride(0), gamma.data_ptr(), (float)eps,
+                                 (const int8_t*)q.data_ptr(), q.stride(0), s.data_ptr<float>(),
+                                 y.data_ptr(), y.stride(0), M, n_q, n_k, K, ws.data_ptr(),
+                                 ws.numel(), cur_stream(x)),
+               "fp_rmsnorm_qkv_w8");
+  return y;
+}
+
+at::Tensor rmsnorm_gate_up_silu_w8(const at::Tensor& x, const at::Tensor& gamma, double eps,
+                                   const at::Tensor& qg, const at::Tensor& sg,
+                                   const at::Tensor& qu, const at::Tensor& su) {
+  check_2d(x, "x", at::kBFloat16);
+  check_2d(qg, "qg", at::kChar);
+  check_2d(qu, "qu", at::kChar);
+  check_scale(sg, qg, "sg");
+  check_scale(su, qu, "su");
+  const int64_t M = x.size(0), K = x.size(1), N = qg.size(0);
+  check_gamma(gamma, K);
+  const c10::DeviceGuard guard(x.device());
+  at::Tensor y = at::empty({M, N}, x.options());
+  at::Tensor ws = norm_workspace(x, M, N, K, true, true);
+  check_status(fp_rmsnorm_gate_up_silu_w8(x.data_ptr(), x.stride(0), gamma.data_ptr(),
+                                          (float)eps, (const int8_t*)qg.data_ptr(), qg.stride(0),
+                                          sg.data_ptr<float>(), (const int8_t*)qu.data_ptr(),
+                                          qu.stride(0), su.data_ptr<float>(), y.data_ptr(),
+                                          y.stride(0), M, N, K, ws.data_ptr(), ws.numel(),
+                                          cur_stream(x)),
+               "fp_rmsnorm_gate_up_silu_w8");
+  return y;
+}
+
 std::tuple<at::Tensor, at::Tensor> quantize_w8(const at::Tensor& w) {
   check_2d(w, "W", at::kBFloat16);
   const c10::DeviceGuard guard(w.device());
@@ -155,6 +256,12 @@ TORCH_LIBRARY(llms_amd, m) {
   m.def("gate_up_silu_w8(Tensor x, Tensor qg, Tensor sg, Tensor qu, Tensor su) -> Tensor");
   m.def("linear(Tensor x, Tensor w) -> Tensor");
   m.def("linear_w8(Tensor x, Tensor q, Tensor scale) -> Tensor");
+  m.def("rmsnorm_qkv(Tensor x, Tensor gamma, float eps, Tensor w, int n_q, int n_k) -> Tensor");
+  m.def("rmsnorm_gate_up_silu(Tensor x, Tensor gamma, float eps, Tensor wg, Tensor wu) -> Tensor");
+  m.def("rmsnorm_qkv_w8(Tensor x, Tensor gamma, float eps, Tensor q, Tensor scale, int n_q, "
+        "int n_k) -> Tensor");
+  m.def("rmsnorm_gate_up_silu_w8(Tensor x, Tensor gamma, float eps, Tensor qg, Tensor sg, "
+        "Tensor qu, Tensor su) -> Tensor");
   m.def("quantize_w8(Tensor w) -> (Tensor, Tensor)");
 }
 
@@ -165,5 +272,9 @@ TORCH_LIBRARY_IMPL(llms_amd, CUDA, m) {
   m.impl("gate_up_silu_w8", gate_up_silu_w8);
   m.impl("linear", linear);
   m.impl("linear_w8", linear_w8);
+  m.impl("rmsnorm_qkv", rmsnorm_qkv);
+  m.impl("rmsnorm_gate_up_silu", rmsnorm_gate_up_silu);
+  m.impl("rmsnorm_qkv_w8", rmsnorm_qkv_w8);
+  m.impl("rmsnorm_gate_up_silu_w8", rmsnorm_gate_up_silu_w8);
   m.impl("quantize_w8", quantize_w8);
 }

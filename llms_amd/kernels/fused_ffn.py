@@ -102,6 +102,8 @@ class TritonFFN(nn.Module):
 
     ``from_eager(..., int8=True)`` keeps per-row int8 gate/up weights
     (``qg``, ``sg``, ``qu``, ``su`` buffers) and runs the int8 kernel.
+    ``prenorm`` (set by ``apply_triton_kernels(..., fuse_norm=True)``) is the
+    block's pre-FFN RMSNorm, run inside the projection call.
     """
 
     def __init__(self, hidden_size: int, intermediate_size: int) -> None:
@@ -110,9 +112,20 @@ class TritonFFN(nn.Module):
         self.up = nn.Linear(hidden_size, intermediate_size, bias=False)
         self.down = nn.Linear(intermediate_size, hidden_size, bias=False)
         self.int8 = False
+        self.prenorm = None
 
     def gate_up(self, x: torch.Tensor) -> torch.Tensor:
-        """The fused projection alone: ``silu(x Wg^T) * (x Wu^T)``."""
+        """The fused projection alone: ``silu(x Wg^T) * (x Wu^T)`` (of the
+        RMS-normalised x when a ``prenorm`` was fused in)."""
+        pn = getattr(self, "prenorm", None)
+        if pn is not None:
+            from .fused_norm import fused_rmsnorm_gate_up_silu, fused_rmsnorm_gate_up_silu_w8
+
+            if self.int8:
+                return fused_rmsnorm_gate_up_silu_w8(x, pn.weight, pn.eps, self.qg, self.sg,
+                                                     self.qu, self.su)
+            return fused_rmsnorm_gate_up_silu(x, pn.weight, pn.eps, self.gate.weight,
+                                              self.up.weight)
         if self.int8:
             return fused_gate_up_silu_w8(x, self.qg, self.sg, self.qu, self.su)
         return triton_fused_gate_up_silu(x, self.gate.weight, self.up.weight)
@@ -129,6 +142,7 @@ class TritonFFN(nn.Module):
         nn.Module.__init__(out)
         out.down = eager.down
         out.int8 = bool(int8)
+        out.prenorm = None
         if out.int8:
             from .quant import quantize_w8_per_row
 

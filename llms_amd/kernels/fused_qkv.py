@@ -130,6 +130,8 @@ class TritonAttention(nn.Module):
 
     With ``from_eager(..., int8=True)`` the stacked weight is kept as
     per-row int8 (``q_qkv``, ``s_qkv`` buffers) and the int8 kernel runs.
+    ``prenorm`` (set by ``apply_triton_kernels(..., fuse_norm=True)``) is the
+    block's pre-attention RMSNorm, run inside the projection call.
     """
 
     def __init__(
@@ -154,6 +156,7 @@ class TritonAttention(nn.Module):
         self.q_norm = RMSNorm(head_dim, eps=rms_eps)
         self.k_norm = RMSNorm(head_dim, eps=rms_eps)
         self.int8 = False
+        self.prenorm = None
 
     @classmethod
     def from_eager(cls, eager: nn.Module, *, int8: bool = False) -> "TritonAttention":
@@ -185,10 +188,20 @@ class TritonAttention(nn.Module):
         out.o = eager.o
         out.q_norm = eager.q_norm
         out.k_norm = eager.k_norm
+        out.prenorm = None
         return out
 
     def project(self, x: torch.Tensor):
-        """The fused projection alone: ``(q, k, v)`` flat views."""
+        """The fused projection alone: ``(q, k, v)`` flat views (of the
+        RMS-normalised x when a ``prenorm`` was fused in)."""
+        pn = getattr(self, "prenorm", None)
+        if pn is not None:
+            from .fused_norm import fused_rmsnorm_qkv, fused_rmsnorm_qkv_w8
+
+            if self.int8:
+                return fused_rmsnorm_qkv_w8(x, pn.weight, pn.eps, self.q_qkv, self.s_qkv,
+                                            n_q=self.n_q, n_k=self.n_k)
+            return fused_rmsnorm_qkv(x, pn.weight, pn.eps, self.W_qkv, n_q=self.n_q, n_k=self.n_k)
         if self.int8:
             return fused_qkv_w8(x, self.q_qkv, self.s_qkv, n_q=self.n_q, n_k=self.n_k)
         return triton_fused_qkv(x, self.W_qkv, n_q=self.n_q, n_k=self.n_k)

@@ -27,6 +27,7 @@ def apply_triton_kernels(
     fused_qkv: bool = True,
     int8: bool = False,
     linear_down_o: bool = False,
+    fuse_norm: bool = False,
 ) -> nn.Module:
     """Replace ``block.ffn`` / ``block.attn`` of every ``model.layers`` block
     with ``TritonFFN`` / ``TritonAttention`` (reference ``swap.py:22-46``).
@@ -35,13 +36,23 @@ def apply_triton_kernels(
     (not in the reference) builds the int8 weight-only modules instead.
     ``linear_down_o=True`` (not in the reference) also replaces each block's
     ``ffn.down`` and ``attn.o`` Linears with :class:`FusedLinear`, int8 when
-    ``int8`` is set.
+    ``int8`` is set. ``fuse_norm=True`` (not in the reference) moves each
+    block's ``norm1`` / ``norm2`` RMSNorm into the fused QKV / gate-up module
+    (``prenorm``) and leaves ``nn.Identity`` in its place, so the norm runs
+    inside the projection call; the block's forward is unchanged.
     """
     for block in model.layers:
         if fused_ffn and not isinstance(block.ffn, TritonFFN):
             block.ffn = TritonFFN.from_eager(block.ffn, int8=int8)
         if fused_qkv and not isinstance(block.attn, TritonAttention):
             block.attn = TritonAttention.from_eager(block.attn, int8=int8)
+        if fuse_norm:
+            if isinstance(block.attn, TritonAttention) and not isinstance(block.norm1, nn.Identity):
+                block.attn.prenorm = block.norm1
+                block.norm1 = nn.Identity()
+            if isinstance(block.ffn, TritonFFN) and not isinstance(block.norm2, nn.Identity):
+                block.ffn.prenorm = block.norm2
+                block.norm2 = nn.Identity()
         if linear_down_o:
             if not isinstance(block.ffn.down, FusedLinear):
                 block.ffn.down = FusedLinear.from_linear(block.ffn.down, int8=int8)

@@ -17,6 +17,9 @@ those of the torch path the reference runs when the fused kernels are off:
   rounded g, ``y = bf16(s * u)``.
 - plain projections ``down`` / ``o`` (``src/engine/model.py:37``,
   ``src/engine/attention.py:183``): ``y = bf16(x . W^T)``.
+- RMSNorm prologue (``src/engine/attention.py:28-33``, applied before QKV and
+  gate-up in ``src/engine/model.py:57-66``): fp32 statistics, then
+  ``bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))``.
 - int8 weight-only (no reference counterpart; the reference names weight
   quantisation as future work only, reference ``DESIGN.md:120``): per output row
   ``s_r = max|w_r| / 127`` (fp32), ``q = clamp(rint(w / s_r), -127, 127)``;
@@ -161,7 +164,7 @@ def _check_gate_up_args(x_shape, wg_shape, wu_shape) -> None:
 
 
 def ref_qkv_full(x_bits: np.ndarray, w_bits: np.ndarray, n_q: int, n_k: int,
-                 tau: float = TAU_SUM) -> OracleOut:
+                 tau: float = TAU_SUM, extra: np.ndarray | None = None) -> OracleOut:
     """The fused QKV output y [..., n_q+2n_k] (before the split).
 
     Follows src/kernels/fused_qkv.py:108-148: validate, flatten the leading
@@ -173,7 +176,10 @@ def ref_qkv_full(x_bits: np.ndarray, w_bits: np.ndarray, n_q: int, n_k: int,
     K = w_bits.shape[1]
     x2 = x_bits.reshape(-1, K)
     acc = exact_linear(x2, w_bits)
-    lo, hi = _candidates(acc, tau * term_norm(x2, w_bits))
+    delta = tau * term_norm(x2, w_bits)
+    if extra is not None:  # admissible spread of the inputs (a prologue's rounding)
+        delta = delta + extra.reshape(delta.shape)
+    lo, hi = _candidates(acc, delta)
     central = round_bf16_f64(acc)
     shp = (*lead, w_bits.shape[0])
     return OracleOut(central.reshape(shp), lo.reshape(shp), hi.reshape(shp))
@@ -208,7 +214,9 @@ def _silu_candidates(g_vals: np.ndarray, tau_s: float):
 
 
 def ref_gate_up_silu_full(x_bits: np.ndarray, wg_bits: np.ndarray, wu_bits: np.ndarray,
-                          tau: float = TAU_SUM, tau_s: float = TAU_SILU) -> OracleOut:
+                          tau: float = TAU_SUM, tau_s: float = TAU_SILU,
+                          extra_g: np.ndarray | None = None,
+                          extra_u: np.ndarray | None = None) -> OracleOut:
     """silu(x.Wg^T) * (x.Wu^T) with the torch bf16 rounding points.
 
     Follows src/engine/model.py:37 (F.silu(self.gate(x)) * self.up(x)) and the
@@ -226,8 +234,14 @@ def ref_gate_up_silu_full(x_bits: np.ndarray, wg_bits: np.ndarray, wu_bits: np.n
     s_c = round_bf16_f64(silu_f64(g_c))
     central = round_bf16_f64(s_c * u_c)  # product of two bf16 is exact in fp64
     # hull over admissible roundings of g, u and silu(g)
-    g_lo, g_hi = _candidates(g, tau * term_norm(x2, wg_bits))
-    u_lo, u_hi = _candidates(u, tau * term_norm(x2, wu_bits))
+    dg = tau * term_norm(x2, wg_bits)
+    du = tau * term_norm(x2, wu_bits)
+    if extra_g is not None:
+        dg = dg + extra_g.reshape(dg.shape)
+    if extra_u is not None:
+        du = du + extra_u.reshape(du.shape)
+    g_lo, g_hi = _candidates(g, dg)
+    u_lo, u_hi = _candidates(u, du)
     lo = np.full(g.shape, np.inf)
     hi = np.full(g.shape, -np.inf)
     for gv in (g_lo, g_hi):
@@ -244,6 +258,65 @@ def ref_gate_up_silu_full(x_bits: np.ndarray, wg_bits: np.ndarray, wu_bits: np.n
 def ref_gate_up_silu(x_bits, wg_bits, wu_bits) -> np.ndarray:
     """bf16 bits of F.silu(F.linear(x, Wg)) * F.linear(x, Wu)."""
     return ref_gate_up_silu_full(x_bits, wg_bits, wu_bits).bits
+
+
+# ------------------------------------------------------------ RMSNorm prologue
+
+# Relative half-width of the window of x * r in which its bf16 rounding is
+# implementation-defined: the fp32 mean of squares depends on the summation
+# order (a few ulps for K <= 2^16), r = 1 / sqrt(var + eps) halves that, and
+# rsqrt implementations differ by about an ulp.
+TAU_NORM = 2.0 ** -18
+
+
+@dataclass
+class NormOut:
+    """Normalised rows: bf16 bits of the central value, and per element the
+    spread |hi - lo| of the admissible values (0 where the rounding of x * r is
+    unambiguous)."""
+
+    bits: np.ndarray
+    spread: np.ndarray
+
+
+def ref_rmsnorm(x_bits: np.ndarray, w_bits: np.ndarray, eps: float,
+                tau: float = TAU_NORM) -> NormOut:
+    """RMSNorm of bf16 rows with a bf16 weight, src/engine/attention.py:28-33:
+    ``x32 = x.float(); var = x32.pow(2).mean(-1); x32 = x32 * rsqrt(var + eps);
+    return weight * x32.to(bf16)``. The statistics are evaluated exactly and
+    rounded once to fp32; every later step is the fp32 / bf16 operation torch
+    performs."""
+    x = bf16_to_f32(x_bits)
+    K = x.shape[-1]
+    x64 = x.astype(np.float64)
+    var = ((x64 * x64).sum(axis=-1, keepdims=True) / K).astype(np.float32)
+    r = np.float32(1.0) / np.sqrt(var + np.float32(eps))
+    t = (x * r).astype(np.float32)
+    w = bf16_to_f32(w_bits)
+    bits = f32_to_bf16(w * bf16_to_f32(f32_to_bf16(t)))
+    t_lo, t_hi = _candidates(t.astype(np.float64), tau * np.abs(t.astype(np.float64)))
+    y_lo = bf16_to_f32(f32_to_bf16(w * t_lo.astype(np.float32))).astype(np.float64)
+    y_hi = bf16_to_f32(f32_to_bf16(w * t_hi.astype(np.float32))).astype(np.float64)
+    return NormOut(bits, np.abs(y_hi - y_lo))
+
+
+def ref_rmsnorm_qkv_full(x_bits, g_bits, eps: float, w_bits, n_q: int, n_k: int) -> OracleOut:
+    """The fused norm + QKV call: the QKV contract on the normalised rows, its
+    hull widened by the norm's admissible spread times |W|."""
+    nrm = ref_rmsnorm(x_bits, g_bits, eps)
+    K = w_bits.shape[1]
+    extra = nrm.spread.reshape(-1, K) @ np.abs(_as_f64(w_bits)).T
+    return ref_qkv_full(nrm.bits, w_bits, n_q, n_k, extra=extra)
+
+
+def ref_rmsnorm_gate_up_silu_full(x_bits, g_bits, eps: float, wg_bits, wu_bits) -> OracleOut:
+    """The fused norm + gate-up-SiLU call (see :func:`ref_rmsnorm_qkv_full`)."""
+    nrm = ref_rmsnorm(x_bits, g_bits, eps)
+    K = wg_bits.shape[1]
+    sp = nrm.spread.reshape(-1, K)
+    return ref_gate_up_silu_full(nrm.bits, wg_bits, wu_bits,
+                                 extra_g=sp @ np.abs(_as_f64(wg_bits)).T,
+                                 extra_u=sp @ np.abs(_as_f64(wu_bits)).T)
 
 
 # ---------------------------------------------------------- int8 weights

@@ -7,6 +7,8 @@ kernels are not swapped in, restated as pure functions:
   equivalently one ``F.linear`` on the row-stacked weight then ``split``
   (``src/bench/microbench_fused_qkv.py:101-103``, ``src/kernels/fused_qkv.py:148``).
 - gate-up-SiLU: ``F.silu(self.gate(x)) * self.up(x)`` (``src/engine/model.py:37``).
+- RMSNorm: ``RMSNorm.forward`` (``src/engine/attention.py:28-33``), applied
+  before QKV and gate-up (``src/engine/model.py:57-66``).
 - down / o: ``self.down(...)`` (``src/engine/model.py:37``) and ``self.o(attn)``
   (``src/engine/attention.py:183``), bias-free ``F.linear``.
 - int8 weight-only: dequantise to bf16, then the calls above (the task's
@@ -35,6 +37,14 @@ def torch_qkv_3(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.T
 def torch_gate_up_silu(x: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor) -> torch.Tensor:
     """``F.silu(F.linear(x, Wg)) * F.linear(x, Wu)``."""
     return F.silu(F.linear(x, wg)) * F.linear(x, wu)
+
+
+def torch_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    orig_dtype = x.dtype
+    x32 = x.float()
+    var = x32.pow(2).mean(-1, keepdim=True)
+    x32 = x32 * torch.rsqrt(var + eps)
+    return weight * x32.to(orig_dtype)
 
 
 def torch_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:

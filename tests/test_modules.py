@@ -125,6 +125,26 @@ def test_apply_linear_down_o_swaps_and_keeps_keys():
         FusedLinear.from_linear(nn.Linear(4, 4, bias=True))
 
 
+def test_apply_fuse_norm_moves_the_norms():
+    """``fuse_norm=True`` hands each block's norm1 / norm2 module to the fused
+    QKV / gate-up module (``prenorm``) and leaves ``nn.Identity`` behind;
+    again is a no-op; without the fused modules nothing moves."""
+    m = tiny_model(TINY, device="cpu")
+    norms = [(b.norm1, b.norm2) for b in m.layers]
+    apply_triton_kernels(m, fuse_norm=True)
+    for (n1, n2), b in zip(norms, m.layers, strict=True):
+        assert isinstance(b.norm1, nn.Identity) and isinstance(b.norm2, nn.Identity)
+        assert b.attn.prenorm is n1 and b.ffn.prenorm is n2
+    apply_triton_kernels(m, fuse_norm=True)
+    assert all(b.attn.prenorm is n1 and b.ffn.prenorm is n2
+               for (n1, n2), b in zip(norms, m.layers, strict=True))
+    keys = set(m.state_dict())
+    assert "layers.0.attn.prenorm.weight" in keys and "layers.0.norm1.weight" not in keys
+    m = apply_triton_kernels(tiny_model(TINY, device="cpu"), fused_ffn=False, fused_qkv=False,
+                             fuse_norm=True)
+    assert not any(isinstance(b.norm1, nn.Identity) for b in m.layers)
+
+
 def test_prewarm_no_op_without_fused_modules():
     """Reference ``test_kernels_fused_ffn.py:395-406``: a model with no
     fused modules (and no ``.layers``) is walked without error."""
@@ -173,6 +193,43 @@ def test_module_logits_match(which, c):
     print(f"\n{which} {c.hidden_size}: max |logit diff| {diff:.4f} (tol {tol:.4f})")
     assert diff <= tol
     assert le[0, -1].argmax().item() == lf[0, -1].argmax().item()
+
+
+def _random_norm_state(c: Cfg, seed: int):
+    st = tiny_state(c, seed=seed)
+    g = torch.Generator().manual_seed(seed + 100)
+    for k in list(st):
+        if k.endswith(("norm1.weight", "norm2.weight")):
+            st[k] = 1.0 + 0.3 * torch.randn(st[k].shape, generator=g)
+    return st
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kw", [dict(fuse_norm=True),
+                                dict(fuse_norm=True, linear_down_o=True),
+                                dict(fuse_norm=True, int8=True)],
+                         ids=["norm", "norm+down_o", "norm+int8"])
+@pytest.mark.parametrize("c", [TINY, WIDE], ids=["tiny", "wide"])
+def test_fused_norm_module_logits(kw, c):
+    """With the norms fused into the projections (non-trivial norm weights),
+    prefill logits and the last-token argmax agree with the eager model; int8
+    compares against the same model without the norm fusion (the weights are
+    quantised either way)."""
+    st = _random_norm_state(c, seed=7)
+    T = 8 if c is TINY else 300
+    ids = torch.randint(0, c.vocab_size, (1, T), generator=torch.Generator().manual_seed(6)).to(DEV)
+    if kw.get("int8"):
+        base = apply_triton_kernels(tiny_model(c, state=st, device=DEV), int8=True)
+    else:
+        base = tiny_model(c, state=st, device=DEV)
+    fused = apply_triton_kernels(tiny_model(c, state=st, device=DEV), **kw)
+    assert all(b.attn.prenorm is not None for b in fused.layers)
+    lb = _logits(base, ids, max_seq=T + 4).float()
+    lf = _logits(fused, ids, max_seq=T + 4).float()
+    diff = (lb - lf).abs().max().item()
+    print(f"\n{kw} {c.hidden_size}: max |logit diff| {diff:.4f} (tol {_logit_tol(lb):.4f})")
+    assert diff <= _logit_tol(lb)
+    assert lb[0, -1].argmax().item() == lf[0, -1].argmax().item()
 
 
 @pytest.mark.gpu

@@ -184,6 +184,99 @@ def test_linear_matches_torch_bf16_linear(M, K, N):
     assert p.n_outside == 0, p
 
 
+# ------------------------------------------------------------- RMSNorm prologue
+
+
+def _norm_inputs(seed, M, K, std, w_spread=0.3):
+    g = gen(seed)
+    x = randn_bf16(g, M, K, std=std)
+    w = (1.0 + w_spread * torch.randn(K, generator=g)).to(torch.bfloat16)
+    return x, w
+
+
+@pytest.mark.parametrize("M,K,std,eps", [(8, 2560, 3.0, 1e-6), (5, 1024, 0.5, 1.0),
+                                         (4, 4096, 0.01, 1e-6), (3, 200, 1.0, 1e-2)])
+def test_rmsnorm_matches_torch_reference(M, K, std, eps):
+    """The reference's RMSNorm.forward restated in torch on the CPU gives the
+    oracle's central value everywhere except at elements the oracle flags as
+    ambiguous, and there it stays within the flagged spread."""
+    x, w = _norm_inputs(20 + K, M, K, std)
+    out = ref.ref_rmsnorm(bits(x), bits(w), eps)
+    t = tp.torch_rmsnorm(x, w, eps)
+    amb = out.spread > 0
+    assert amb.mean() < 0.01
+    assert np.array_equal(out.bits[~amb], bits(t)[~amb])
+    dv = np.abs(ref.bf16_to_f32(out.bits).astype(np.float64) - ref.bf16_to_f32(bits(t)))
+    assert np.all(dv <= out.spread)
+
+
+def test_rmsnorm_closed_forms():
+    """Rows of a constant c with eps = 0: r = 1/|c| exactly for powers of two,
+    so x * r = sign(c) and the output is sign(c) * w. A one-hot row a e_j:
+    mean(x^2) = a^2 / K, so x_j * r = sign(a) sqrt(K) (exactly 16 for K = 256)."""
+    K = 256
+    w = (1.0 + 0.3 * torch.randn(K, generator=gen(3))).to(torch.bfloat16)
+    x = torch.full((2, K), 4.0, dtype=torch.bfloat16)
+    x[1] = -0.5
+    out = ref.ref_rmsnorm(bits(x), bits(w), 0.0)
+    wf = ref.bf16_to_f32(bits(w))
+    np.testing.assert_array_equal(ref.bf16_to_f32(out.bits[0]), wf)
+    np.testing.assert_array_equal(ref.bf16_to_f32(out.bits[1]), -wf)
+    x = torch.zeros(1, K, dtype=torch.bfloat16)
+    x[0, 7] = -3.0
+    out = ref.ref_rmsnorm(bits(x), bits(w), 0.0)
+    y = ref.bf16_to_f32(out.bits[0])
+    assert y[7] == ref.bf16_to_f32(ref.f32_to_bf16(np.float32(-16.0) * wf[7:8]))[0]
+    assert np.count_nonzero(y) == 1
+
+
+def _mutant_norm_single_rounding(xb, wb, eps):
+    x = ref.bf16_to_f32(xb).astype(np.float64)
+    r = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+    return ref.f32_to_bf16((ref.bf16_to_f32(wb) * x * r).astype(np.float32))
+
+
+def _mutant_norm_unbiased(xb, wb, eps):
+    x = ref.bf16_to_f32(xb)
+    K = x.shape[-1]
+    var = ((x.astype(np.float64) ** 2).sum(-1, keepdims=True) / (K - 1)).astype(np.float32)
+    t = x * (np.float32(1) / np.sqrt(var + np.float32(eps)))
+    return ref.f32_to_bf16(ref.bf16_to_f32(wb) * ref.bf16_to_f32(ref.f32_to_bf16(t)))
+
+
+def test_rmsnorm_mutants_fail_the_pins():
+    x, w = _norm_inputs(30, 16, 1024, 2.0)
+    t = bits(tp.torch_rmsnorm(x, w, 1e-6))
+    out = ref.ref_rmsnorm(bits(x), bits(w), 1e-6)
+    ok = out.spread == 0
+    for mutant in (_mutant_norm_single_rounding, _mutant_norm_unbiased):
+        mb = mutant(bits(x), bits(w), 1e-6)
+        assert np.count_nonzero(mb[ok] != t[ok]) > 50, mutant
+    # eps matters when it is not negligible against mean(x^2)
+    x, w = _norm_inputs(31, 4, 512, 0.5)
+    assert not np.array_equal(ref.ref_rmsnorm(bits(x), bits(w), 0.0).bits,
+                              bits(tp.torch_rmsnorm(x, w, 1.0)))
+
+
+@pytest.mark.parametrize("M,K,N", [(4, 2560, 96), (3, 1024, 64)])
+def test_fused_norm_oracles_hold_the_torch_path(M, K, N):
+    """RMSNorm then F.linear / silu-gate-up in bf16 on the CPU (the reference's
+    norm1 -> q/k/v and norm2 -> gate/up) lands inside the fused oracles'
+    hulls everywhere."""
+    x, w = _norm_inputs(40 + K, M, K, 2.0)
+    _, wq = qkv_inputs(41, M, K, N - 32, 16)
+    xn = tp.torch_rmsnorm(x, w, 1e-6)
+    q, k, v = tp.torch_qkv(xn, wq, N - 32, 16)
+    out = ref.ref_rmsnorm_qkv_full(bits(x), bits(w), 1e-6, bits(wq), N - 32, 16)
+    p = _hull_contains(np.concatenate([bits(q), bits(k), bits(v)], axis=-1), out)
+    assert p.n_outside == 0, p
+    _, wg, wu = ffn_inputs(42, M, K, N, w_std=0.05)
+    y = tp.torch_gate_up_silu(xn, wg, wu)
+    out = ref.ref_rmsnorm_gate_up_silu_full(bits(x), bits(w), 1e-6, bits(wg), bits(wu))
+    p = _hull_contains(bits(y), out)
+    assert p.n_outside == 0, p
+
+
 # ------------------------------------------------------------- brute force
 
 
