@@ -236,6 +236,74 @@ def counters_run(torch, kern, shape, layers: int) -> dict:
     }
 
 
+def decode_run(torch, n_tok: int) -> dict:
+    """Greedy decode of n_tok tokens after a 128-token prefill on a Qwen3-4B-
+    shaped decoder (``llms_amd.harness``, random weights): the reference's
+    eager modules (hipBLASLt ``F.linear``, torch RMSNorm), then the same model
+    after ``apply_triton_kernels(fuse_norm=True, linear_down_o=True)``; each
+    step eagerly and as a replayed HIP graph (``StepGraph``), plus the
+    graph-replayed verify step of 4 and 8 draft tokens. Times are wall-clock
+    per step with the argmax fed back on the device."""
+    from llms_amd.harness import QWEN3_4B, StepGraph, random_model
+    from llms_amd.kernels import apply_triton_kernels
+
+    c = QWEN3_4B
+    P = 128
+    # room for the longest run (verify T = 8: (n_tok + 2) steps of 8) plus
+    # StepGraph's scratch positions at the end of the cache
+    S = P + (n_tok + 4) * 8 + 16
+    assert S <= c.max_position_embeddings
+    log(f"decode: building a random Qwen3-4B-shaped model ({c.num_hidden_layers} layers)")
+    m = random_model(c, seed=0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    prompt = torch.randint(0, c.vocab_size, (1, P), generator=g, device="cuda")
+
+    def prefill():
+        cache = m.alloc_cache(S)
+        with torch.inference_mode():
+            logits = m(prompt, cache, start_pos=0)
+        return cache, logits[:, -1:].argmax(-1)
+
+    def eager_ms():
+        cache, nt = prefill()
+        with torch.inference_mode():
+            for i in range(2):  # warm-up steps
+                nt = m(nt, cache, start_pos=P + i)[:, -1:].argmax(-1)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(n_tok):
+                nt = m(nt, cache, start_pos=P + 2 + i)[:, -1:].argmax(-1)
+            torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n_tok * 1e3
+
+    def graph_ms(T: int):
+        cache, nt = prefill()
+        step = StepGraph(m, cache, T=T)
+        ids = nt.repeat(1, T)
+        for i in range(2):
+            step(ids, P + i * T)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(n_tok):
+            ids = step(ids, P + (2 + i) * T)[:, -1:].argmax(-1).repeat(1, T)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n_tok * 1e3
+
+    out = {"mode": "decode", "model": "qwen3-4b shapes, random weights", "prompt": P,
+           "tokens": n_tok, "ms_per_token": {}, "verify_ms_per_step": {}}
+    out["ms_per_token"]["reference_eager"] = round(eager_ms(), 3)
+    out["ms_per_token"]["reference_graph"] = round(graph_ms(1), 3)
+    log("decode: reference path timed; swapping in the fused modules")
+    apply_triton_kernels(m, fuse_norm=True, linear_down_o=True)
+    out["ms_per_token"]["fused_eager"] = round(eager_ms(), 3)
+    out["ms_per_token"]["fused_graph"] = round(graph_ms(1), 3)
+    for T in (4, 8):
+        out["verify_ms_per_step"][f"fused_graph_T{T}"] = round(graph_ms(T), 3)
+    out["tokens_per_s"] = {k: round(1e3 / v, 1) for k, v in out["ms_per_token"].items()}
+    return out
+
+
 def linear_run(torch, kern, M: int, N: int, K: int, reps: int) -> dict:
     """The plain projection y = x W^T (the engine's down / o Linears) over
     weight sets cycled past the Infinity Cache: average launch duration by
@@ -271,6 +339,11 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--counters", action="store_true",
                     help="run only the short fixed sequence used for rocprofv3 --pmc runs")
+    ap.add_argument("--decode", action="store_true",
+                    help="end-to-end decode on a Qwen3-4B-shaped harness model with random "
+                         "weights: reference eager path vs fused modules, eager and "
+                         "graph-replayed steps; prints one JSON line")
+    ap.add_argument("--decode-tokens", type=int, default=32)
     ap.add_argument("--linear", metavar="M,N,K",
                     help="time only the plain projection (down / o) of this shape over "
                          "cycled weight sets and print one JSON line (profiling aid)")
@@ -298,6 +371,9 @@ def main() -> int:
     L = args.layers
     if args.counters:
         print(json.dumps(counters_run(torch, kern, shape, L)), flush=True)
+        return 0
+    if args.decode:
+        print(json.dumps(decode_run(torch, args.decode_tokens)), flush=True)
         return 0
     if args.linear:
         M, N, Kl = (int(v) for v in args.linear.split(","))

@@ -46,6 +46,25 @@ def rotate_half(t: torch.Tensor) -> torch.Tensor:
     return torch.cat((-t[..., h:], t[..., :h]), dim=-1)
 
 
+def write_kv(cache_k: torch.Tensor, cache_v: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+             start_pos):
+    """Store k, v [B, H, T, D] at positions start_pos .. start_pos+T-1 of the
+    layer's cache [max_batch, H, max_seq, D] and return the keys/values the
+    queries attend over: positions 0 .. start_pos+T-1 for an int start_pos
+    (the reference's slicing, ``src/engine/attention.py:132-136``), the whole
+    cache for a device-tensor start_pos (masked by ``attend``)."""
+    B, T = k.shape[0], k.shape[2]
+    if torch.is_tensor(start_pos):
+        idx = start_pos + torch.arange(T, device=k.device)
+        cache_k[:B].index_copy_(2, idx, k)
+        cache_v[:B].index_copy_(2, idx, v)
+        return cache_k[:B], cache_v[:B]
+    end = start_pos + T
+    cache_k[:B, :, start_pos:end, :] = k
+    cache_v[:B, :, start_pos:end, :] = v
+    return cache_k[:B, :, :end, :], cache_v[:B, :, :end, :]
+
+
 def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
     """q, k [B, H, T, D]; cos, sin [T, D]."""
     c = cos[None, None]
@@ -53,13 +72,16 @@ def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.T
     return q * c + rotate_half(q) * s, k * c + rotate_half(k) * s
 
 
-def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos: int) -> torch.Tensor:
+def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos) -> torch.Tensor:
     """Causal softmax attention of queries at positions start_pos .. start_pos+T-1
-    over keys/values at positions 0 .. S-1.
+    over keys/values at positions 0 .. S-1. ``start_pos`` may also be a 0-dim
+    device tensor (a step captured in a HIP graph and replayed at any
+    position): the mask is then built on the device and always applied, so S
+    may be the whole cache.
 
     q [B, H, T, D]; k, v [B, H, S, D] (GQA heads already expanded). Same
     result as the reference's three ``scaled_dot_product_attention`` branches
-    (``src/engine/attention.py:173-181``: no mask for T == 1, ``is_causal`` at
+    (``src/engine/attention.py:152-160``: no mask for T == 1, ``is_causal`` at
     start_pos 0, an explicit ``q_pos >= k_pos`` mask otherwise), which all
     reduce to "key position <= query position" with scale D^-0.5.
 
@@ -70,7 +92,11 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos: int) ->
     T, S = q.shape[2], k.shape[2]
     scores = torch.matmul(q.float().contiguous(), k.float().transpose(-2, -1).contiguous())
     scores = scores * (q.shape[-1] ** -0.5)
-    if T > 1:
+    if torch.is_tensor(start_pos):
+        q_pos = (start_pos + torch.arange(T, device=q.device))[:, None]
+        k_pos = torch.arange(S, device=q.device)[None, :]
+        scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
+    elif T > 1:
         q_pos = torch.arange(start_pos, start_pos + T, device=q.device)[:, None]
         k_pos = torch.arange(S, device=q.device)[None, :]
         scores = scores.masked_fill(k_pos > q_pos, float("-inf"))

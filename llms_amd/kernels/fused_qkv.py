@@ -16,7 +16,7 @@ from torch import nn
 
 from .. import _lib
 from ._checks import inner_contiguous, require_bf16_hip, require_device
-from ._eager import RMSNorm, apply_rope, attend
+from ._eager import RMSNorm, apply_rope, attend, write_kv
 
 
 def triton_fused_qkv(
@@ -218,7 +218,8 @@ class TritonAttention(nn.Module):
     ) -> torch.Tensor:
         # The reference forward (src/kernels/fused_qkv.py:242-282) with the
         # fused HIP projection in place of the Triton call and attend() in
-        # place of its three SDPA branches.
+        # place of its three SDPA branches. start_pos may be a 0-dim device
+        # tensor (a step captured in a HIP graph, replayed at any position).
         B, T, _ = x.shape
         q_flat, k_flat, v_flat = self.project(x)
         q = q_flat.view(B, T, self.num_heads, self.head_dim)
@@ -230,11 +231,7 @@ class TritonAttention(nn.Module):
         v = v.transpose(1, 2)
         q, k = apply_rope(q, k, cos, sin)
 
-        end_pos = start_pos + T
-        kv_cache.k[layer_idx][:B, :, start_pos:end_pos, :] = k
-        kv_cache.v[layer_idx][:B, :, start_pos:end_pos, :] = v
-        full_k = kv_cache.k[layer_idx][:B, :, :end_pos, :]
-        full_v = kv_cache.v[layer_idx][:B, :, :end_pos, :]
+        full_k, full_v = write_kv(kv_cache.k[layer_idx], kv_cache.v[layer_idx], k, v, start_pos)
 
         n_rep = self.num_heads // self.num_kv_heads
         if n_rep > 1:

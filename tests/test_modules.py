@@ -1,6 +1,6 @@
 """Module-level drop-in tests: ``TritonAttention``, ``TritonFFN``,
 ``apply_triton_kernels`` and ``prewarm_triton_kernels`` inside a tiny synthetic
-Qwen3 engine (``tests/_tiny_qwen3.py``).
+Qwen3 engine (``llms_amd/harness.py``).
 
 Mirrors the reference's engine-integration tests, which need network weights
 (Qwen3-0.6B) and so cannot run here; the tiny model stands in for them:
@@ -30,7 +30,7 @@ from torch import nn
 
 from llms_amd.kernels import (FusedLinear, TritonAttention, TritonFFN, apply_triton_kernels,
                               prewarm_triton_kernels)
-from tests._tiny_qwen3 import Cfg, greedy_generate, teacher_forced_logits, tiny_model, tiny_state
+from llms_amd.harness import Cfg, greedy_generate, teacher_forced_logits, tiny_model, tiny_state
 
 DEV = "cuda"
 
