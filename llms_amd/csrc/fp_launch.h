@@ -37,8 +37,8 @@ int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s);
 
 // Row-streaming kernels for 1 <= M <= kRowsMaxM (fp_rows.hip), bf16 and
 // int8, used by launch_stream when rows_supported() holds. x is staged in
-// LDS (M rounded up to 1, 2 or 4 rows, K to whole chunks): at most
-// kRowsMaxLds bytes.
+// LDS (M rounded up to 1, 2 or 4 rows, K to whole chunks; one more row for
+// a fused norm weight): at most kRowsMaxLds bytes.
 constexpr int64_t kRowsMaxM = 4;
 constexpr int64_t kRowsMaxLds = 65536;
 template <bool W8>
@@ -47,9 +47,10 @@ bool rows_supported(const StreamArgs& a, bool aligned);
 // launch for the RMSNorm prologue and the projection).
 template <bool GATEUP, bool W8>
 int launch_rows(const StreamArgs& a, hipStream_t s);
-// Whether M x K fits the rows kernel's x staging (shape only; alignment and
-// the M limit of rows_supported apply on top).
-bool rows_fit(int64_t M, int64_t K, bool w8);
+// Whether M x K fits the rows kernel's x staging, with the norm weight's row
+// when norm is set (shape only; alignment and the M limit of rows_supported
+// apply on top).
+bool rows_fit(int64_t M, int64_t K, bool w8, bool norm);
 
 // RMSNorm prologue on its own (fp_norm.h): xn [M, K] (row stride K) from x.
 int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* gamma, float eps,

@@ -111,23 +111,58 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   const int64_t Kp = (int64_t)J * KC;
   const int64_t nvec = MM * (Kp / 8);
   if constexpr (NORM) {
-    // every workgroup computes the same per-row scales (fixed-order sums)
-    __shared__ float red[NW];
-    __shared__ float rinv[MM];
+    // One pass over global memory: the raw x rows and the norm weight (an
+    // extra LDS row after the MM x rows) go to LDS while each thread sums
+    // the squares of its x elements; then the per-row scales (fixed-order
+    // sums, the same in every workgroup) and the rows normalised in place.
+    __shared__ float red[MM * NW];
+    uint16_t* gs = xs + MM * Kp;
+    float s[MM];
 #pragma unroll
-    for (int m = 0; m < MM; ++m) {
-      if (m < a.M) {
-        const float ss = row_sumsq<NW * kWave, true>(a.x + m * a.ldx, K, red);
-        if (threadIdx.x == 0) rinv[m] = rms_scale(ss, K, a.eps);
+    for (int m = 0; m < MM; ++m) s[m] = 0.f;
+    for (int64_t i = threadIdx.x; i < nvec + Kp / 8; i += NW * kWave) {
+      const int64_t m = i / (Kp / 8), k = (i - m * (Kp / 8)) * 8;
+      u32x4 v = {0, 0, 0, 0};
+      if (m < a.M) v = load_bf16x8<true>(a.x + m * a.ldx, k, K);
+      else if (m == MM) v = load_bf16x8<true>(a.gamma, k, K);
+      *reinterpret_cast<u32x4*>(xs + i * 8) = v;
+      if (m < MM) {
+        float q = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = bf16_bits_to_f32(v[j] & 0xffffu), hi = bf16_bits_to_f32(v[j] >> 16);
+          q += __fmul_rn(lo, lo);
+          q += __fmul_rn(hi, hi);
+        }
+#pragma unroll
+        for (int j = 0; j < MM; ++j)
+          if (m == j) s[j] += q;
       }
     }
+#pragma unroll
+    for (int m = 0; m < MM; ++m) s[m] = wave_sum(s[m]);
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MM; ++m) red[m * NW + wave] = s[m];
+    }
     __syncthreads();
+    float rinv[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) t += red[m * NW + w];
+      rinv[m] = rms_scale(t, K, a.eps);
+    }
     for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave) {
       const int64_t m = i / (Kp / 8), k = (i - m * (Kp / 8)) * 8;
-      *reinterpret_cast<u32x4*>(xs + i * 8) =
-          m < a.M ? norm_bf16x8(load_bf16x8<true>(a.x + m * a.ldx, k, K),
-                                load_bf16x8<true>(a.gamma, k, K), rinv[m])
-                  : u32x4{0, 0, 0, 0};
+      if (m >= a.M) continue;
+      float r = rinv[0];
+#pragma unroll
+      for (int j = 1; j < MM; ++j)
+        if (m == j) r = rinv[j];
+      u32x4* p = reinterpret_cast<u32x4*>(xs + i * 8);
+      *p = norm_bf16x8(*p, *reinterpret_cast<const u32x4*>(gs + k), r);
     }
   } else {
     for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave) {
@@ -211,17 +246,18 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
 // x rows staged per workgroup: M rounded up to 1, 2 or 4
 inline int64_t rows_mm(int64_t M) { return M <= 2 ? M : 4; }
 
-// LDS bytes of the staged x: MM rows of K rounded up to whole chunks
+// LDS bytes of the staged x: MM rows of K rounded up to whole chunks, plus
+// one such row for the norm weight when the RMSNorm prologue is fused in
 template <bool W8>
-int64_t rows_lds_bytes(int64_t M, int64_t K) {
+int64_t rows_lds_bytes(int64_t M, int64_t K, bool norm = false) {
   constexpr int KC = kc<W8>();
-  return rows_mm(M) * ((K + KC - 1) / KC) * KC * 2;
+  return (rows_mm(M) + (norm ? 1 : 0)) * ((K + KC - 1) / KC) * KC * 2;
 }
 
 template <int NW, int R, int U, int MM, bool GATEUP, bool W8>
 int launch_rows_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t per = (int64_t)NW * R;
-  const size_t shm = (size_t)rows_lds_bytes<W8>(MM, a.K);
+  const size_t shm = (size_t)rows_lds_bytes<W8>(MM, a.K, a.gamma != nullptr);
   const dim3 grid((unsigned)((a.N + per - 1) / per)), block(NW * kWave);
   if (a.gamma)
     hipLaunchKernelGGL((rows_kernel<NW, R, U, MM, GATEUP, W8, true>), grid, block, shm, s, a);
@@ -252,8 +288,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* x, int64_t
 // bf16 takes M <= 2 here (for 3..4 rows the 8-row streaming kernel is
 // faster: its MFMA columns hold the x rows), int8 up to kRowsMaxM (the
 // dequantisation, shared by all x rows, dominates).
-bool rows_fit(int64_t M, int64_t K, bool w8) {
-  return (w8 ? rows_lds_bytes<true>(M, K) : rows_lds_bytes<false>(M, K)) <= kRowsMaxLds;
+bool rows_fit(int64_t M, int64_t K, bool w8, bool norm) {
+  return (w8 ? rows_lds_bytes<true>(M, K, norm) : rows_lds_bytes<false>(M, K, norm)) <= kRowsMaxLds;
 }
 
 int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* gamma, float eps,
@@ -270,7 +306,8 @@ int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* gamma, float 
 template <bool W8>
 bool rows_supported(const StreamArgs& a, bool aligned) {
   const int64_t max_m = W8 ? kRowsMaxM : 2;
-  return aligned && a.M >= 1 && a.M <= max_m && rows_lds_bytes<W8>(a.M, a.K) <= kRowsMaxLds;
+  return aligned && a.M >= 1 && a.M <= max_m &&
+         rows_lds_bytes<W8>(a.M, a.K, a.gamma != nullptr) <= kRowsMaxLds;
 }
 
 template bool rows_supported<false>(const StreamArgs&, bool);
