@@ -167,6 +167,41 @@ int fp_linear_bf16_ws(const void* x, int64_t ldx,
                       void* stream);
 
 /*
+ * Workspace variants of the int8 entry points (no reference counterpart). For
+ * calls with enough rows (fp_workspace_bytes_w8(M, N, K, gate_up) > 0: from
+ * 48 rows for one weight stream; 48-64 and from 256 or 512 rows for gate-up),
+ * given that much
+ * workspace, the int8 weights are dequantised once into the workspace as
+ * bf16(q * s) — the exact weight the int8 contract computes with — and the
+ * bf16 MFMA path (k split across workgroups included) runs on them; results
+ * stay within the same contract. Without a workspace, or with fewer rows, the
+ * in-register dequantising kernels of the plain entry points run.
+ */
+int64_t fp_workspace_bytes_w8(int64_t M, int64_t N, int64_t K, int gate_up);
+
+int fp_qkv_w8_ws(const void* x, int64_t ldx,
+                 const int8_t* q, int64_t ldq, const float* scale,
+                 void* y, int64_t ldy,
+                 int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+                 void* workspace, int64_t workspace_bytes,
+                 void* stream);
+
+int fp_gate_up_silu_w8_ws(const void* x, int64_t ldx,
+                          const int8_t* qg, int64_t ldqg, const float* sg,
+                          const int8_t* qu, int64_t ldqu, const float* su,
+                          void* y, int64_t ldy,
+                          int64_t M, int64_t N, int64_t K,
+                          void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+int fp_linear_w8_ws(const void* x, int64_t ldx,
+                    const int8_t* q, int64_t ldq, const float* scale,
+                    void* y, int64_t ldy,
+                    int64_t M, int64_t N, int64_t K,
+                    void* workspace, int64_t workspace_bytes,
+                    void* stream);
+
+/*
  * RMSNorm prologue fused with the projections (no reference counterpart as a
  * kernel: it replaces the eager pair norm1(x) -> attention q/k/v and
  * norm2(h) -> FFN gate/up, reference src/engine/model.py:57-66 with RMSNorm
@@ -177,7 +212,8 @@ int fp_linear_bf16_ws(const void* x, int64_t ldx,
  * (the row-streaming regime: bf16 M <= 2, int8 M <= 4, with room for x in
  * LDS) run as one launch that normalises x while staging it; the others need
  * fp_rmsnorm_workspace_bytes(M, N, K, gate_up, int8) bytes of workspace
- * (the normalised rows, then any split-k partials) and return
+ * (the normalised rows, then any split-k partials, or for int8 calls with
+ * enough rows the dequantised weights as in fp_qkv_w8_ws) and return
  * FP_ERR_WORKSPACE without it. eps must be finite and >= 0.
  */
 int64_t fp_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up, int int8);

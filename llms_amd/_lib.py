@@ -43,6 +43,11 @@ CAPI_SIGNATURES: dict[str, list] = {
     "fp_qkv_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "fp_gate_up_silu_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "fp_linear_bf16_ws": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "fp_workspace_bytes_w8": [_I64, _I64, _I64, ctypes.c_int],
+    "fp_qkv_w8_ws": [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
+    "fp_gate_up_silu_w8_ws": [_P, _I64, _P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P,
+                              _I64, _P],
+    "fp_linear_w8_ws": [_P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "fp_rmsnorm_workspace_bytes": [_I64, _I64, _I64, ctypes.c_int, ctypes.c_int],
     "fp_rmsnorm_qkv_bf16": [_P, _I64, _P, _F, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "fp_rmsnorm_gate_up_silu_bf16": [_P, _I64, _P, _F, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64,
@@ -83,6 +88,7 @@ def capi() -> ctypes.CDLL:
                 fn.argtypes = argtypes
                 fn.restype = {"fp_status_string": ctypes.c_char_p,
                               "fp_workspace_bytes": ctypes.c_int64,
+                              "fp_workspace_bytes_w8": ctypes.c_int64,
                               "fp_rmsnorm_workspace_bytes": ctypes.c_int64}.get(name, ctypes.c_int)
             _capi = lib
         return _capi

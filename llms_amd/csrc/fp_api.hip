@@ -34,6 +34,23 @@ __global__ __launch_bounds__(256) void quantize_w8_kernel(const uint16_t* w, int
   }
 }
 
+// bf16(q * s[row]) for 16 weights per thread (K % 16 == 0, 16-byte-aligned
+// rows): the weight the int8 kernels compute with, written as a bf16 matrix
+// [N, K] (row stride K) for the bf16 MFMA path.
+__global__ __launch_bounds__(256) void dequant_w8_kernel(const int8_t* q, int64_t ldq,
+                                                         const float* scale, uint16_t* w,
+                                                         int64_t N, int64_t K) {
+  const int64_t per_row = K / 16;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= N * per_row) return;
+  const int64_t r = t / per_row, c = (t - r * per_row) * 16;
+  const u32x4 v = ld16(q + r * ldq + c);
+  const float sc = scale[r], n128 = -128.f * sc;
+  uint16_t* out = w + r * K + c;
+  *reinterpret_cast<u32x4*>(out) = dequant8_bf16(v.x, v.y, sc, n128);
+  *reinterpret_cast<u32x4*>(out + 8) = dequant8_bf16(v.z, v.w, sc, n128);
+}
+
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // rc is the hipError_t of the launch (hipGetLastError right after it).
@@ -53,6 +70,62 @@ int run(const StreamArgs& a, bool aligned, hipStream_t s) {
 }
 
 inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// int8 calls with enough rows and a workspace: the weights are dequantised
+// once into the workspace and the bf16 path runs on them. The extra 3 bytes
+// per weight pay for themselves once the in-register int8 kernels are
+// compute-bound. Measured on MI355X (Qwen3-4B/8B): one weight stream (QKV,
+// down, o) from 48 rows (4B QKV at 48 rows: 23 vs 37 us; 4B down at 128:
+// 42 vs 226 us; QKV at 2048: 77 vs 133 us). Gate-up at 48-64 rows (the int8
+// streaming kernel's weakest range: 4B 74 vs 94 us at 64), then again from
+// 256 rows, or 512 above 2^26 weights; in between the int8 LDS tiles hold up
+// (8B gate-up at 256: 151 vs 143 us; at 2048: 397 vs 776 us).
+inline int64_t dequant_bytes(int64_t N, int64_t K, bool gateup) {
+  return round_up(N * K * 2, 256) * (gateup ? 2 : 1);
+}
+
+inline bool use_dequant(int64_t M, int64_t N, int64_t K, bool gateup) {
+  if (K % 16 != 0 || M < 48) return false;
+  if (!gateup || M <= kStreamMaxM) return true;
+  return M >= (2 * N * K > ((int64_t)1 << 26) ? 512 : 256);
+}
+
+template <bool GATEUP>
+int run_w8(const StreamArgs& a, bool aligned, void* ws, int64_t ws_bytes, hipStream_t s) {
+  if (a.M == 0) return FP_OK;
+  const int64_t wb = dequant_bytes(a.N, a.K, GATEUP);
+  if (aligned && use_dequant(a.M, a.N, a.K, GATEUP) && ws && ws_bytes >= wb) {
+    uint16_t* w0 = (uint16_t*)ws;
+    uint16_t* w1 = GATEUP ? (uint16_t*)((char*)ws + wb / 2) : nullptr;
+    const unsigned blocks = (unsigned)((a.N * (a.K / 16) + 255) / 256);
+    hipLaunchKernelGGL(dequant_w8_kernel, dim3(blocks), dim3(256), 0, s, (const int8_t*)a.w0,
+                       a.ldw0, a.s0, w0, a.N, a.K);
+    if constexpr (GATEUP)
+      hipLaunchKernelGGL(dequant_w8_kernel, dim3(blocks), dim3(256), 0, s, (const int8_t*)a.w1,
+                         a.ldw1, a.s1, w1, a.N, a.K);
+    int rc = (int)hipGetLastError();
+    if (rc) return launch_status(rc);
+    StreamArgs b = a;
+    b.w0 = w0;
+    b.ldw0 = a.K;
+    b.w1 = w1;
+    b.ldw1 = GATEUP ? a.K : 0;
+    b.s0 = b.s1 = nullptr;
+    b.ws = (float*)((char*)ws + wb);
+    b.ws_floats = (ws_bytes - wb) / 4;
+    return run<GATEUP, false>(b, true, s);
+  }
+  StreamArgs b = a;
+  b.ws = nullptr;
+  b.ws_floats = 0;
+  return run<GATEUP, true>(b, aligned, s);
+}
+
+int64_t w8_workspace_bytes(int64_t M, int64_t N, int64_t K, bool gateup) {
+  if (M < 1 || N < 1 || K < 1 || !use_dequant(M, N, K, gateup)) return 0;
+  return dequant_bytes(N, K, gateup) +
+         4 * gemm_split_ws_floats(gemm_split_plan(M, N, K, gateup), M, N, K, gateup);
+}
 
 // RMSNorm prologue + projection: one launch on the rows kernel (x normalised
 // while it is staged in LDS), else the norm into the workspace and the plain
@@ -75,9 +148,11 @@ int run_norm(StreamArgs a, bool xaligned, bool waligned, void* ws, int64_t ws_by
   b.x = xn;
   b.ldx = a.K;
   b.gamma = nullptr;
-  b.ws = W8 ? nullptr : (float*)((char*)ws + xn_bytes);
-  b.ws_floats = W8 ? 0 : (ws_bytes - xn_bytes) / 4;
-  return run<GATEUP, W8>(b, waligned && a.K % (W8 ? 16 : 8) == 0, s);
+  const bool baligned = waligned && a.K % (W8 ? 16 : 8) == 0;
+  if constexpr (W8) return run_w8<GATEUP>(b, baligned, (char*)ws + xn_bytes, ws_bytes - xn_bytes, s);
+  b.ws = (float*)((char*)ws + xn_bytes);
+  b.ws_floats = (ws_bytes - xn_bytes) / 4;
+  return run<GATEUP, false>(b, baligned, s);
 }
 
 int check_norm(float eps, void* ws, int64_t ws_bytes) {
@@ -114,7 +189,7 @@ const char* fp_status_string(int status) {
   }
 }
 
-int fp_abi_version(void) { return (1 << 16) | 3; }
+int fp_abi_version(void) { return (1 << 16) | 4; }
 
 int64_t fp_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up) {
   if (M < 1 || N < 1 || K < 1) return 0;
@@ -169,36 +244,56 @@ int fp_gate_up_silu_bf16(const void* x, int64_t ldx, const void* wg, int64_t ldw
                                  stream);
 }
 
-int fp_qkv_w8(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,
-              void* y, int64_t ldy, int64_t M, int64_t n_q, int64_t n_k, int64_t K,
-              void* stream) {
+int64_t fp_workspace_bytes_w8(int64_t M, int64_t N, int64_t K, int gate_up) {
+  return fp::w8_workspace_bytes(M, N, K, gate_up != 0);
+}
+
+int fp_qkv_w8_ws(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,
+                 void* y, int64_t ldy, int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+                 void* workspace, int64_t workspace_bytes, void* stream) {
   if (n_q < 1 || n_k < 0) return FP_ERR_SHAPE;
   const int64_t N = n_q + 2 * n_k;
   int st = fp::check_common(M, N, K, ldx, ldy);
   if (st) return st;
   if (ldq < K) return FP_ERR_STRIDE;
+  if (workspace_bytes < 0 || (workspace && !fp::al16(workspace))) return FP_ERR_WORKSPACE;
   if (M == 0) return FP_OK;
   if (!x || !q || !scale || !y) return FP_ERR_NULL;
   StreamArgs a{(const uint16_t*)x, ldx, q, ldq, nullptr, 0, scale, nullptr,
                (uint16_t*)y, ldy, M, N, K};
   const bool aligned = (K % 16 == 0) && (ldx % 8 == 0) && (ldq % 16 == 0) &&
                        fp::al16(x) && fp::al16(q);
-  return fp::run<false, true>(a, aligned, (hipStream_t)stream);
+  return fp::run_w8<false>(a, aligned, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
-int fp_gate_up_silu_w8(const void* x, int64_t ldx, const int8_t* qg, int64_t ldqg,
-                       const float* sg, const int8_t* qu, int64_t ldqu, const float* su,
-                       void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
+int fp_qkv_w8(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,
+              void* y, int64_t ldy, int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+              void* stream) {
+  return fp_qkv_w8_ws(x, ldx, q, ldq, scale, y, ldy, M, n_q, n_k, K, nullptr, 0, stream);
+}
+
+int fp_gate_up_silu_w8_ws(const void* x, int64_t ldx, const int8_t* qg, int64_t ldqg,
+                          const float* sg, const int8_t* qu, int64_t ldqu, const float* su,
+                          void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                          void* workspace, int64_t workspace_bytes, void* stream) {
   int st = fp::check_common(M, N, K, ldx, ldy);
   if (st) return st;
   if (ldqg < K || ldqu < K) return FP_ERR_STRIDE;
+  if (workspace_bytes < 0 || (workspace && !fp::al16(workspace))) return FP_ERR_WORKSPACE;
   if (M == 0) return FP_OK;
   if (!x || !qg || !sg || !qu || !su || !y) return FP_ERR_NULL;
   StreamArgs a{(const uint16_t*)x, ldx, qg, ldqg, qu, ldqu, sg, su,
                (uint16_t*)y, ldy, M, N, K};
   const bool aligned = (K % 16 == 0) && (ldx % 8 == 0) && (ldqg % 16 == 0) &&
                        (ldqu % 16 == 0) && fp::al16(x) && fp::al16(qg) && fp::al16(qu);
-  return fp::run<true, true>(a, aligned, (hipStream_t)stream);
+  return fp::run_w8<true>(a, aligned, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int fp_gate_up_silu_w8(const void* x, int64_t ldx, const int8_t* qg, int64_t ldqg,
+                       const float* sg, const int8_t* qu, int64_t ldqu, const float* su,
+                       void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
+  return fp_gate_up_silu_w8_ws(x, ldx, qg, ldqg, sg, qu, ldqu, su, y, ldy, M, N, K, nullptr, 0,
+                               stream);
 }
 
 int fp_linear_bf16(const void* x, int64_t ldx, const void* w, int64_t ldw, void* y, int64_t ldy,
@@ -217,15 +312,22 @@ int fp_linear_w8(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const
   return fp_qkv_w8(x, ldx, q, ldq, scale, y, ldy, M, N, 0, K, stream);
 }
 
+int fp_linear_w8_ws(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, const float* scale,
+                    void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+  return fp_qkv_w8_ws(x, ldx, q, ldq, scale, y, ldy, M, N, 0, K, workspace, workspace_bytes,
+                      stream);
+}
+
 int64_t fp_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up, int int8) {
   if (M < 1 || N < 1 || K < 1) return 0;
   const bool w8 = int8 != 0;
   if (M <= (w8 ? fp::kRowsMaxM : 2) && K % (w8 ? 16 : 8) == 0 && fp::rows_fit(M, K, w8, true))
     return 0;
   int64_t b = fp::round_up(M * K * 2, 256);
-  if (!w8) b += 4 * fp::gemm_split_ws_floats(fp::gemm_split_plan(M, N, K, gate_up != 0), M, N, K,
-                                             gate_up != 0);
-  return b;
+  if (w8) return b + fp::w8_workspace_bytes(M, N, K, gate_up != 0);
+  return b + 4 * fp::gemm_split_ws_floats(fp::gemm_split_plan(M, N, K, gate_up != 0), M, N, K,
+                                          gate_up != 0);
 }
 
 int fp_rmsnorm_qkv_bf16(const void* x, int64_t ldx, const void* gamma, float eps, const void* w,

@@ -40,26 +40,6 @@ namespace {
 template <bool W8>
 constexpr int kc() { return W8 ? 1024 : 512; }
 
-typedef __attribute__((ext_vector_type(2))) float f32x2;
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-
-// Four int8 of one dword dequantised to bf16(q * s) and returned as two
-// packed bf16 pairs (bytes 0,1 and 2,3): fma(q + 128, s, -128 s) is the exact
-// product rounded once to fp32, the conversion is RNE.
-__device__ __forceinline__ u32x2 dequant4_bf16(uint32_t qword, float s, float n128s) {
-  const uint32_t u = qword ^ 0x80808080u;
-  const f32x2 lo = {fmaf((float)(u & 0xffu), s, n128s), fmaf((float)((u >> 8) & 0xffu), s, n128s)};
-  const f32x2 hi = {fmaf((float)((u >> 16) & 0xffu), s, n128s), fmaf((float)(u >> 24), s, n128s)};
-  return u32x2{__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
-               __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2))};
-}
-
-// Eight int8 (two dwords) dequantised to eight packed bf16(q * s).
-__device__ __forceinline__ u32x4 dequant8_bf16(uint32_t q0, uint32_t q1, float s, float n128s) {
-  const u32x2 lo = dequant4_bf16(q0, s, n128s), hi = dequant4_bf16(q1, s, n128s);
-  return u32x4{lo.x, lo.y, hi.x, hi.y};
-}
-
 // Diagonal of a wave's 16x16 MFMA accumulator: lane l holds rows
 // 4 (l / 16) + r, column l % 16, so D[i][i] sits in lane 20 (i / 4) + i % 4,
 // register i % 4. Returns it there and 0 elsewhere.

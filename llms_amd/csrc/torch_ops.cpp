@@ -36,6 +36,13 @@ at::Tensor workspace(const at::Tensor& x, int64_t M, int64_t N, int64_t K, bool 
   return at::empty({bytes}, x.options().dtype(at::kByte));
 }
 
+// Workspace for an int8 call: the dequantised weights (and split partials)
+// from 128 rows, empty below.
+at::Tensor workspace_w8(const at::Tensor& x, int64_t M, int64_t N, int64_t K, bool gate_up) {
+  const int64_t bytes = fp_workspace_bytes_w8(M, N, K, gate_up ? 1 : 0);
+  return at::empty({bytes}, x.options().dtype(at::kByte));
+}
+
 at::Tensor qkv(const at::Tensor& x, const at::Tensor& w, int64_t n_q, int64_t n_k) {
   check_2d(x, "x", at::kBFloat16);
   check_2d(w, "W_qkv", at::kBFloat16);
@@ -76,10 +83,11 @@ at::Tensor qkv_w8(const at::Tensor& x, const at::Tensor& q, const at::Tensor& s,
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = q.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
-  check_status(fp_qkv_w8(x.data_ptr(), x.stride(0), (const int8_t*)q.data_ptr(), q.stride(0),
-                         s.data_ptr<float>(), y.data_ptr(), y.stride(0), M, n_q, n_k, K,
-                         cur_stream(x)),
-               "fp_qkv_w8");
+  at::Tensor ws = workspace_w8(x, M, N, K, false);
+  check_status(fp_qkv_w8_ws(x.data_ptr(), x.stride(0), (const int8_t*)q.data_ptr(), q.stride(0),
+                            s.data_ptr<float>(), y.data_ptr(), y.stride(0), M, n_q, n_k, K,
+                            ws.numel() ? ws.data_ptr() : nullptr, ws.numel(), cur_stream(x)),
+               "fp_qkv_w8_ws");
   return y;
 }
 
@@ -95,12 +103,14 @@ at::Tensor gate_up_silu_w8(const at::Tensor& x, const at::Tensor& qg, const at::
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = qg.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
-  check_status(fp_gate_up_silu_w8(x.data_ptr(), x.stride(0), (const int8_t*)qg.data_ptr(),
-                                  qg.stride(0), sg.data_ptr<float>(),
-                                  (const int8_t*)qu.data_ptr(), qu.stride(0),
-                                  su.data_ptr<float>(), y.data_ptr(), y.stride(0), M, N, K,
-                                  cur_stream(x)),
-               "fp_gate_up_silu_w8");
+  at::Tensor ws = workspace_w8(x, M, N, K, true);
+  check_status(fp_gate_up_silu_w8_ws(x.data_ptr(), x.stride(0), (const int8_t*)qg.data_ptr(),
+                                     qg.stride(0), sg.data_ptr<float>(),
+                                     (const int8_t*)qu.data_ptr(), qu.stride(0),
+                                     su.data_ptr<float>(), y.data_ptr(), y.stride(0), M, N, K,
+                                     ws.numel() ? ws.data_ptr() : nullptr, ws.numel(),
+                                     cur_stream(x)),
+               "fp_gate_up_silu_w8_ws");
   return y;
 }
 
@@ -127,10 +137,11 @@ at::Tensor linear_w8(const at::Tensor& x, const at::Tensor& q, const at::Tensor&
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = q.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
-  check_status(fp_linear_w8(x.data_ptr(), x.stride(0), (const int8_t*)q.data_ptr(), q.stride(0),
-                            s.data_ptr<float>(), y.data_ptr(), y.stride(0), M, N, K,
-                            cur_stream(x)),
-               "fp_linear_w8");
+  at::Tensor ws = workspace_w8(x, M, N, K, false);
+  check_status(fp_linear_w8_ws(x.data_ptr(), x.stride(0), (const int8_t*)q.data_ptr(), q.stride(0),
+                               s.data_ptr<float>(), y.data_ptr(), y.stride(0), M, N, K,
+                               ws.numel() ? ws.data_ptr() : nullptr, ws.numel(), cur_stream(x)),
+               "fp_linear_w8_ws");
   return y;
 }
 

@@ -440,6 +440,42 @@ def test_split_k_across_workgroups(M, N, K, op):
     _check(y.cpu()[rows], ref.ref_linear(bits(x)[rows], bits(w)), f"split {op} M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("M,K,N,op,dq", [(47, 2560, 6144, "qkv", False), (48, 2560, 6144, "qkv", True),
+                                         (64, 1040, 1001, "gate-up", True),
+                                         (200, 1040, 1001, "gate-up", False),
+                                         (256, 1040, 1001, "gate-up", True),
+                                         (512, 9728, 2560, "linear", True),
+                                         (300, 2560, 9728, "gate-up", True)])
+def test_int8_dequantised_mfma_path(M, K, N, op, dq):
+    """With enough rows the int8 calls dequantise the weights into the
+    workspace and run the bf16 path (split across workgroups where planned);
+    the contract is unchanged. Below the threshold the in-register int8
+    kernels run."""
+    from llms_amd import _lib
+
+    gu = op == "gate-up"
+    assert (_lib.capi().fp_workspace_bytes_w8(M, N, K, int(gu)) > 0) == dq
+    kern = _kernels()
+    rows = _rows(M, limit=64)
+    if gu:
+        x, wg, wu = ffn_inputs(170 + M, M, K, N)
+        qg, sg = _quant(wg)
+        qu, su = _quant(wu)
+        y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+        out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                           qu.cpu().numpy(), su.cpu().numpy())
+    else:
+        x, w = qkv_inputs(180 + M, M, K, N, 0)
+        q, s = _quant(w)
+        if op == "qkv":
+            n_k = N // 6
+            y = torch.cat(kern.fused_qkv_w8(x.to(DEV), q, s, n_q=N - 2 * n_k, n_k=n_k), dim=-1).cpu()
+        else:
+            y = kern.fused_linear_w8(x.to(DEV), q, s).cpu()
+        out = ref.ref_linear_w8(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy())
+    _check(y[rows], out, f"int8 {op} M={M} K={K} N={N}")
+
+
 @pytest.mark.parametrize("M", [1, 4, 64, 2048])
 def test_linear_int8(M):
     K, N = 9728, 2560
