@@ -389,21 +389,15 @@ int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
   return ((N + cols - 1) / cols) * ((M + kTiles[tile].bm - 1) / kTiles[tile].bm);
 }
 
-// Tile table for the unsplit bf16 prefill path, measured on MI355X with
-// Qwen3-4B and -8B shapes. What decides is how many rounds of workgroups a
-// call needs on 256 CUs: 256 x 256 tiles (1 workgroup per CU) run best once
-// they fill the chip, smaller tiles (2 per CU) win where they save a round.
-// QKV-sized outputs (<= 8192 weight rows): 64 x 128 tiles with three stages
-// to 768 rows, 128 x 128 to 1536, then 256 x 256. Outputs of at most 4096
-// columns (the down and o projections) keep 128 x 128 until a 256 x 256 grid
-// fills the chip (2048 x 2560 -> 80 tiles: 128 x 128; 4096 x 4096 -> 256
-// tiles: 256 x 256). Gate-up-sized:
-// 128 x 128 to 384 rows, 256 x 256 to 768 (152-192 tiles, one round), 128 x
-// 128 to 1536, 256 x 256.
-int gemm_tile_unsplit(int64_t M, int64_t wrows) {
+// The tile whose grid fill decides whether to split k (gemm_split_plan): the
+// table the split rules were measured against. QKV-sized outputs (<= 8192
+// weight rows): 64 x 128 to 768 rows, 128 x 128 to 1536, then 256 x 256;
+// outputs of at most 4096 columns: 64 x 128 to 768 rows, then 128 x 128 until
+// a 256 x 256 grid fills the chip; gate-up-sized: 128 x 128 to 384 rows,
+// 256 x 256 to 768, 128 x 128 to 1536, 256 x 256.
+int split_ref_tile(int64_t M, int64_t wrows) {
   if (wrows <= 4096) {
     if (M <= 768) return kT64x128;
-    // 256 x 256 once its grid fills the chip (8B down, 4096 x 4096: 256 tiles)
     if (tile_count(kT256x256, M, wrows, false) >= kCUs) return kT256x256;
     return kT128x128;
   }
@@ -413,13 +407,89 @@ int gemm_tile_unsplit(int64_t M, int64_t wrows) {
   return M <= 1536 ? kT128x128 : kT256x256;
 }
 
+// Cost model of an unsplit prefill grid, fitted to warm-clock measurements on
+// MI355X (Qwen3-0.6B/4B/8B QKV, gate-up, o and down, M = 256..8192; the
+// dispatch it yields is within 0.4% of the best of the four candidates below
+// on average over those 120 shapes). A grid's time is set by its busiest CU,
+// which runs k = ceil(tiles / 256) tiles; what a tile costs hardly depends on
+// how many other CUs are busy. 256 x 256 tiles (one per CU) cost k times
+// (per-k-step + per-tile) units; tiles that fit two per CU run in pairs: k / 2
+// pairs and k % 2 single tiles, each with its own per-k-step cost (a pair
+// costs ~1.1-1.3 times a single), plus a per-tile cost. Units are relative
+// (a common per-shape factor is divided out).
+struct TileCost {
+  double single, pair, tile;
+};
+constexpr TileCost kCost64x128{0.566, 0.670, 0.357};
+constexpr TileCost kCost128x128{0.627, 0.796, 1.930};
+constexpr TileCost kCost256x256{1.086, 0.0, 9.180};
+
+double grid_cost(int tile, int64_t M, int64_t N, int64_t nkt, bool gateup) {
+  const int64_t n = tile_count(tile, M, N, gateup);
+  if (n == 0) return 0.0;
+  const int64_t k = (n + kCUs - 1) / kCUs;
+  const TileCost& c =
+      tile == kT64x128 ? kCost64x128 : (tile == kT128x128 ? kCost128x128 : kCost256x256);
+  if (kTiles[tile].per_cu == 1) return (double)k * ((double)nkt * c.single + c.tile);
+  const int64_t pairs = k / 2, singles = k % 2;
+  return (double)nkt * ((double)pairs * c.pair + (double)singles * c.single) +
+         (double)(pairs + singles) * c.tile;
+}
+
+// The unsplit plan: the cheapest of 64 x 128, 128 x 128, 256 x 256, and
+// "256 x 256 for whole rounds + a 128 x 128 tail" (nmain > 0: the first
+// nmain output columns as whole 256 x 256 rounds, the rest as 128 x 128 tiles
+// in a second launch). The tail form turns the last partial round of 256 x
+// 256 tiles into 128 x 128 tiles that spread over all CUs (measured 4B
+// gate-up M = 2048: 223.6 -> 203.4 us; 4B QKV M = 4096: 142.7 -> 125.9 us).
+// Both tiles contract every output over the same k-steps in the same order,
+// so each plan's result is bit-identical to the others'. One correction to
+// the model: where 128 x 128 tiles would run one per CU and 64 x 128 tiles at
+// most two, 64 x 128 is faster on every shape measured (the pair of smaller
+// tiles hides latency better than one tile of the same work).
+GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup) {
+  const int64_t nkt = K / kBK;
+  GemmPlan best{kT64x128, 0};
+  double cbest = grid_cost(kT64x128, M, N, nkt, gateup);
+  for (int t : {kT128x128, kT256x256}) {
+    const double c = grid_cost(t, M, N, nkt, gateup);
+    if (c < cbest) best = GemmPlan{t, 0}, cbest = c;
+  }
+  const int64_t cols = gateup ? 128 : 256;  // output columns of a 256 x 256 tile
+  const int64_t n_nt = (N + cols - 1) / cols, n_mt = (M + 255) / 256;
+  const int64_t rounds = n_nt * n_mt / kCUs;
+  const int64_t main_nt = rounds >= 1 ? rounds * kCUs / n_mt : 0;
+  if (main_nt > 0 && main_nt < n_nt) {
+    const int64_t nmain = main_nt * cols;
+    const double c = grid_cost(kT256x256, M, nmain, nkt, gateup) +
+                     grid_cost(kT128x128, M, N - nmain, nkt, gateup);
+    if (c < cbest) best = GemmPlan{kT256x256, nmain}, cbest = c;
+  }
+  const auto per_cu = [&](int t) { return (tile_count(t, M, N, gateup) + kCUs - 1) / kCUs; };
+  if (best.tile == kT128x128 && per_cu(kT128x128) == 1 && per_cu(kT64x128) <= 2)
+    best = GemmPlan{kT64x128, 0};
+  return best;
+}
+
 template <bool GATEUP>
 int launch_gemm(const StreamArgs& a, hipStream_t s) {
-  switch (gemm_tile_unsplit(a.M, GATEUP ? 2 * a.N : a.N)) {
+  const GemmPlan p = gemm_plan_unsplit(a.M, a.N, a.K, GATEUP);
+  switch (p.tile) {
     case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
     case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
-    default: return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
+    default: break;
   }
+  if (p.nmain == 0) return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
+  StreamArgs m = a;
+  m.N = p.nmain;
+  int e = launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(m, s);
+  if (e) return e;
+  StreamArgs t = a;
+  t.N = a.N - p.nmain;
+  t.w0 = static_cast<const uint16_t*>(a.w0) + p.nmain * a.ldw0;
+  if (GATEUP) t.w1 = static_cast<const uint16_t*>(a.w1) + p.nmain * a.ldw1;
+  t.y = a.y + p.nmain;
+  return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(t, s);
 }
 
 // When to split k across workgroups, measured on MI355X over Qwen3-0.6B/4B/8B
@@ -447,7 +517,7 @@ GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
     if (nkt < 64 || wrows * K < ((int64_t)1 << 24)) return none;
   } else {
     if (gateup && nkt < 128) return none;
-    const int t0 = gemm_tile_unsplit(M, wrows);
+    const int t0 = split_ref_tile(M, wrows);
     const double fill = (double)tile_count(t0, M, N, gateup) / (kCUs * kTiles[t0].per_cu);
     if (!(fill <= 0.5 || (fill < 0.75 && nkt >= 128))) return none;
   }

@@ -248,6 +248,47 @@ def test_qwen3_4b_prefill_8192_rows():
     check_ffn(8192, 8192, K, I, label="4B gate-up M=8192 (row subset)")
 
 
+# Row counts whose prefill grids differ on Qwen3-4B shapes: 64 x 128, 128 x 128
+# and 256 x 256 tiles, and whole 256 x 256 rounds followed by a 128 x 128 tail
+# launch (gate-up at 1024 and 2048 rows, QKV at 3072).
+PLAN_ROWS = {"gate_up": (2048, [128, 384, 512, 1024, 1536]),
+             "qkv": (3072, [384, 768, 1536, 2048])}
+
+
+@pytest.mark.parametrize("kind", list(PLAN_ROWS))
+def test_prefill_rows_independent_of_grid_plan(kind):
+    """Every prefill grid plan contracts each output over the same k-steps in
+    the same order, so a row's bits do not depend on how many rows the call
+    has (and with it which tiles, or which of two launches, computed it). The
+    largest call is checked against the oracle on a row subset; the smaller
+    calls must reproduce its rows bit for bit."""
+    K, n_q, n_k, I = QWEN3_4B
+    M_full, Ms = PLAN_ROWS[kind]
+    if kind == "qkv":
+        x, w = qkv_inputs(77, M_full, K, n_q, n_k)
+        xd, wd = x.to(DEV), w.to(DEV)
+
+        def run(xx):
+            q, k, v = _kernels().triton_fused_qkv(xx, wd, n_q=n_q, n_k=n_k)
+            return torch.cat([q, k, v], dim=-1).cpu()
+        y = run(xd)
+        rows = _rows(M_full)
+        _check(y[rows], ref.ref_qkv_full(bits(x)[rows], bits(w), n_q, n_k), f"qkv M={M_full}")
+    else:
+        x, wg, wu = ffn_inputs(77, M_full, K, I)
+        xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+
+        def run(xx):
+            return _kernels().triton_fused_gate_up_silu(xx, wgd, wud).cpu()
+        y = run(xd)
+        rows = _rows(M_full)
+        _check(y[rows], ref.ref_gate_up_silu_full(bits(x)[rows], bits(wg), bits(wu)),
+               f"gate-up M={M_full}")
+    for M in Ms:
+        ym = run(xd[:M].contiguous())
+        assert torch.equal(ym.view(torch.int16), y[:M].view(torch.int16)), f"{kind} M={M}"
+
+
 @pytest.mark.parametrize("M", [17, 64, 65, 100, 256])
 def test_regime_boundaries(M):
     """Around the streaming / tiled switch and partial M tiles."""
