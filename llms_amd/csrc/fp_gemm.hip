@@ -15,8 +15,9 @@
 //     output sit in adjacent accumulators of one lane; silu(g)*u is applied in
 //     registers at the torch rounding points.
 //   - Workgroups are remapped so that each XCD (its own L2) runs a contiguous
-//     range of tiles, ordered M-fastest: the ~32 tiles an XCD runs at once
-//     share their weight panels and the activation panel in its L2.
+//     range of tiles, ordered in groups of 8 m-tiles, M-fastest inside a
+//     group: the ~32 tiles an XCD runs at once (8 m x 4 n) share their weight
+//     and activation panels in its L2.
 // Requirements (checked by the dispatcher): bf16, K % 64 == 0, 16-byte-aligned
 // rows (the general case runs tiled_kernel).
 #include "fp_common.h"
@@ -29,6 +30,7 @@ namespace {
 constexpr int kBK = 64;          // k per LDS stage
 constexpr int kCPR = kBK / 8;    // 16-byte chunks per tile row
 constexpr int kRPI = 1024 / (kBK * 2);  // tile rows per load instruction
+constexpr int kGroupM = 8;       // m-tiles per group of the tile order
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -82,14 +84,20 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   const int wn = wave / WM, wm = wave % WM;
   const int li = lane & 15, grp = lane >> 4;
 
-  // XCD-aware tile order (see file comment), then M-fastest within an XCD;
-  // with SPLIT the k-range index is the slowest.
+  // XCD-aware tile order (see file comment); with SPLIT the k-range index is
+  // the slowest.
   const int T = (int)gridDim.x;
   int b = blockIdx.x;
   if (T % 8 == 0) b = (b % 8) * (T / 8) + b / 8;
   const int ks = SPLIT ? b / (n_mt * n_nt) : 0;
   b -= ks * n_mt * n_nt;
-  const int tm = b % n_mt, tn = b / n_mt;
+  // Groups of kGroupM m-tiles, M-fastest inside a group: the 32 tiles an XCD
+  // runs at once form an 8 x 4 block (12 operand panels per k-step in its L2)
+  // rather than a strip down one weight panel (33 panels once M > 8 tiles).
+  const int gbase = (b / (kGroupM * n_nt)) * kGroupM;
+  const int gm = n_mt - gbase < kGroupM ? n_mt - gbase : kGroupM;
+  const int gin = b - gbase * n_nt;
+  const int tm = gbase + gin % gm, tn = gin / gm;
   const int64_t m0 = (int64_t)tm * BM;
   const int64_t c0 = (int64_t)tn * (GATEUP ? BN / 2 : BN);  // first output column
 
