@@ -257,20 +257,24 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 #pragma unroll
     for (int i = 0; i < FN; i += (GATEUP ? 2 : 1)) {
       int64_t nb;
-      uint32_t h[4];
+      uint32_t p0, p1;  // packed bf16 of columns nb, nb+1 and nb+2, nb+3
       if constexpr (GATEUP) {
         const int sub = (wn * TN) / 16 + i;  // even: gate group of pair sub/2
         nb = c0 + (sub / 2) * 16 + 4 * grp;
+        uint32_t h[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) h[r] = gate_up_silu_bits(acc[i][j][r], acc[i + 1][j][r]);
+        p0 = h[0] | (h[1] << 16);
+        p1 = h[2] | (h[3] << 16);
       } else {
         nb = c0 + wn * TN + i * 16 + 4 * grp;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16_bits(acc[i][j][r]);
+        p0 = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+        p1 = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
       }
       if (y8 && nb + 3 < a.N) {
-        *reinterpret_cast<u32x2*>(yrow + nb) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        *reinterpret_cast<u32x2*>(yrow + nb) = u32x2{p0, p1};
       } else {
+        const uint32_t h[4] = {p0 & 0xffffu, p0 >> 16, p1 & 0xffffu, p1 >> 16};
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           if (nb + r < a.N) yrow[nb + r] = (uint16_t)h[r];

@@ -161,6 +161,42 @@ def test_qwen3_4b_gate_up_decode(M):
     check_ffn(M, M, K, I)
 
 
+def _bf16_from_bits(b: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(b.astype(np.uint16)).view(np.int16)).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M", [1, 512], ids=["row-kernel", "mfma-grid"])
+def test_gate_up_epilogue_every_bf16_g(M):
+    """Every finite bf16 value of g goes through the silu epilogue: x rows are
+    one-hot and Wu is all ones, so output (m, n) is bf16(silu(g)) with g one
+    chosen weight. M = 1 runs the decode row kernel over 65024 outputs; M = 512
+    with K = 64 runs the MFMA prefill grid, g[m, n] = Wg[n, m % 64]. Checked
+    against the oracle (silu in float64, hull of one fp32 silu rounding)."""
+    b = np.arange(65536, dtype=np.uint32)
+    vals = b[((b >> 7) & 0xFF) != 0xFF].astype(np.uint16)  # the 65024 finite bf16
+    one = np.uint16(0x3F80)
+    K = 64
+    if M == 1:
+        N = vals.size
+        wg = np.zeros((N, K), np.uint16)
+        wg[:, 0] = vals
+        wu = np.zeros((N, K), np.uint16)
+        wu[:, 0] = one
+        x = np.zeros((1, K), np.uint16)
+        x[0, 0] = one
+    else:
+        N = -(-vals.size // K)
+        flat = np.zeros(N * K, np.uint16)
+        flat[: vals.size] = vals
+        wg = flat.reshape(N, K)
+        wu = np.full((N, K), one, np.uint16)
+        x = np.zeros((M, K), np.uint16)
+        x[np.arange(M), np.arange(M) % K] = one
+    xt, wgt, wut = _bf16_from_bits(x), _bf16_from_bits(wg), _bf16_from_bits(wu)
+    y = _kernels().triton_fused_gate_up_silu(xt.to(DEV), wgt.to(DEV), wut.to(DEV)).cpu()
+    _check(y, ref.ref_gate_up_silu_full(x, wg, wu), f"silu epilogue, all bf16 g, M={M}")
+
+
 def test_gate_up_non_pow2_N():
     """N-tail: N=9700 (reference test_triton_bf16_non_pow2_N), and a tile-tail
     N for the prefill kernel."""
