@@ -14,7 +14,7 @@ step time. Also reported: TFLOP/s at M=2048 (prefill), the dominant kernel's
 roofline (per-launch HIP events on its stream), and the reference's unfused
 torch path timed on this host's CPU cores.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 100]
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 
@@ -124,9 +124,17 @@ def kernel_seconds(torch, launches: list, reps: int) -> float:
     time is divided by the number of launches. Graph replay keeps the GPU fed
     back-to-back, so no host launch latency is counted."""
     graph = capture(torch, lambda: [fn() for fn in launches])
-    sec = time_graph(torch, graph, reps, 2)
+    sec = time_graph(torch, graph, reps, warm_replays(torch, graph, 2))
     del graph
     return sec / len(launches)
+
+
+def warm_replays(torch, graph, floor: int) -> int:
+    """Replays that make ~100 ms (at least `floor`): after an idle gap the GPU
+    clocks need that long to settle (a cold 10 ms window reads 5-9% slow on
+    the prefill kernels)."""
+    once = time_graph(torch, graph, 1, 1)
+    return max(floor, int(0.1 / max(once, 1e-6)))
 
 
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -325,11 +333,76 @@ def linear_run(torch, kern, M: int, N: int, K: int, reps: int) -> dict:
             "hipblaslt_us": round(ref * 1e6, 2)}
 
 
+# Every configuration BASELINE.json lists: (model, M, int8).
+CONFIGS = ([("qwen3-0.6b", 1, False)]
+           + [("qwen3-4b", m, False) for m in (1, 3, 4, 8, 512, 2048, 8192)]
+           + [("qwen3-4b", m, True) for m in (1, 4, 2048)]
+           + [("qwen3-8b", m, q) for q in (False, True) for m in (1, 4, 16, 64, 256, 4096)])
+
+
+def configs_run(torch, kern, reps: int):
+    """Both fused projections on every BASELINE configuration, one JSON line
+    each: average launch duration by graph replay over distinct weight sets
+    (36 for M <= 64, else enough to pass the Infinity Cache), GB/s of
+    algorithmic bytes and TFLOP/s; for bf16, torch's F.linear (hipBLASLt) on
+    the same contraction (one GEMM over [Wq; Wk; Wv] or [Wg; Wu], no epilogue)
+    for scale."""
+    import torch.nn.functional as F
+
+    for model, M, int8 in CONFIGS:
+        K, n_q, n_k, inter = SHAPES[model]
+        n = n_q + 2 * n_k
+        wbytes = (1 if int8 else 2) * K * (n + 2 * inter)
+        sets = 36 if M <= 64 else max(4, min(36, (1200 << 20) // wbytes))
+        g = torch.Generator(device="cuda")
+        g.manual_seed(0)
+        x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+
+        def w(rows):
+            return (torch.randn(rows, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+
+        ws = []
+        for _ in range(sets):
+            t = (w(n), w(inter), w(inter))
+            ws.append(tuple(kern.quantize_w8_per_row(v) for v in t) if int8 else t)
+            del t
+        if int8:
+            qk = [lambda t=t: kern.fused_qkv_w8(x, t[0][0], t[0][1], n_q=n_q, n_k=n_k) for t in ws]
+            gu = [lambda t=t: kern.fused_gate_up_silu_w8(x, t[1][0], t[1][1], t[2][0], t[2][1])
+                  for t in ws]
+        else:
+            qk = [lambda t=t: kern.triton_fused_qkv(x, t[0], n_q=n_q, n_k=n_k) for t in ws]
+            gu = [lambda t=t: kern.triton_fused_gate_up_silu(x, t[1], t[2]) for t in ws]
+        tq = kernel_seconds(torch, qk, reps)
+        tg = kernel_seconds(torch, gu, reps)
+        wb = 1 if int8 else 2
+        bq = wb * n * K + (4 * n if int8 else 0) + 2 * M * K + 2 * M * n
+        bg = wb * 2 * inter * K + (8 * inter if int8 else 0) + 2 * M * K + 2 * M * inter
+        out = {"mode": "config", "model": model, "M": M, "weights": "int8" if int8 else "bf16",
+               "weight_sets": sets,
+               "qkv_us": round(tq * 1e6, 2), "qkv_gbs": round(bq / tq / 1e9, 1),
+               "qkv_tflops": round(2 * M * K * n / tq / 1e12, 1),
+               "gate_up_us": round(tg * 1e6, 2), "gate_up_gbs": round(bg / tg / 1e9, 1),
+               "gate_up_tflops": round(2 * M * K * 2 * inter / tg / 1e12, 1)}
+        if not int8:
+            cat_q = [t[0] for t in ws]
+            cat_g = [torch.cat([t[1], t[2]]) for t in ws]
+            out["hipblaslt_qkv_us"] = round(
+                kernel_seconds(torch, [lambda c=c: F.linear(x, c) for c in cat_q], reps) * 1e6, 2)
+            out["hipblaslt_gate_up_us"] = round(
+                kernel_seconds(torch, [lambda c=c: F.linear(x, c) for c in cat_g], reps) * 1e6, 2)
+            del cat_g
+        print(json.dumps(out), flush=True)
+        del ws, qk, gu
+        torch.cuda.empty_cache()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 100 untimed steps of ~0.9 ms: the clocks settle before the timed region
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--model", default="qwen3-4b", choices=sorted(SHAPES))
     ap.add_argument("--prefill-m", type=int, default=2048)
@@ -344,6 +417,9 @@ def main() -> int:
                          "weights: reference eager path vs fused modules, eager and "
                          "graph-replayed steps; prints one JSON line")
     ap.add_argument("--decode-tokens", type=int, default=32)
+    ap.add_argument("--configs", action="store_true",
+                    help="time both projections on every BASELINE configuration (with "
+                         "hipBLASLt for scale); one JSON line per configuration")
     ap.add_argument("--linear", metavar="M,N,K",
                     help="time only the plain projection (down / o) of this shape over "
                          "cycled weight sets and print one JSON line (profiling aid)")
@@ -374,6 +450,9 @@ def main() -> int:
         return 0
     if args.decode:
         print(json.dumps(decode_run(torch, args.decode_tokens)), flush=True)
+        return 0
+    if args.configs:
+        configs_run(torch, kern, args.steps)
         return 0
     if args.linear:
         M, N, Kl = (int(v) for v in args.linear.split(","))
@@ -422,7 +501,7 @@ def main() -> int:
         torch.cuda.synchronize()
         graph = capture(torch, lambda: run_step(stack, kern))
         psteps = max(3, args.steps // 4)
-        psec = time_graph(torch, graph, psteps, max(1, args.warmup // 2))
+        psec = time_graph(torch, graph, psteps, warm_replays(torch, graph, max(1, args.warmup // 2)))
         tflops = L * pair_flops(Mp, K, n_qkv, inter) / psec / 1e12
         dp_gu = kernel_seconds(torch, gu, 3)
         dp_qk = kernel_seconds(torch, qk, 3)

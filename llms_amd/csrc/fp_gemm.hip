@@ -389,11 +389,12 @@ bool gemm_supported(const StreamArgs& a, bool aligned) {
 }
 
 // Tiles the dispatcher uses: {weight rows, x rows, workgroups per CU (LDS)}.
-enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256 };
+enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256, kT192x256 };
 struct TileInfo {
   int bn, bm, per_cu;
 };
-constexpr TileInfo kTiles[] = {{64, 32, 4}, {128, 64, 3}, {64, 128, 2}, {128, 128, 2}, {256, 256, 1}};
+constexpr TileInfo kTiles[] = {{64, 32, 4},   {128, 64, 3},  {64, 128, 2},
+                               {128, 128, 2}, {256, 256, 1}, {192, 256, 1}};
 constexpr int kCUs = 256;
 
 int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
@@ -421,34 +422,40 @@ int split_ref_tile(int64_t M, int64_t wrows) {
 
 // Cost model of an unsplit prefill grid, fitted to warm-clock measurements on
 // MI355X (Qwen3-0.6B/4B/8B QKV, gate-up, o and down, M = 256..8192; the
-// dispatch it yields is within 0.4% of the best of the four candidates below
-// on average over those 120 shapes). A grid's time is set by its busiest CU,
+// dispatch it yields is within 0.1% of the best of the candidates below on
+// average over those 120 shapes, 4% at worst). A grid's time is set by its busiest CU,
 // which runs k = ceil(tiles / 256) tiles; what a tile costs hardly depends on
-// how many other CUs are busy. 256 x 256 tiles (one per CU) cost k times
-// (per-k-step + per-tile) units; tiles that fit two per CU run in pairs: k / 2
-// pairs and k % 2 single tiles, each with its own per-k-step cost (a pair
-// costs ~1.1-1.3 times a single), plus a per-tile cost. Units are relative
-// (a common per-shape factor is divided out).
+// how many other CUs are busy. 256 x 256 and 192 x 256 tiles (one per CU)
+// cost k times (per-k-step + per-tile) units; tiles that fit two per CU run
+// in pairs: k / 2 pairs and k % 2 single tiles, each with its own per-k-step
+// cost (a pair costs ~1.1-1.3 times a single), plus a per-tile cost. Units
+// are relative (a common per-shape factor is divided out). 192 x 256 tiles
+// (3/4 of the work of 256 x 256) take ~0.92 of the time: they pay where their
+// count fills whole rounds (QKV 6144 x 2048: 256 tiles, 69.4 -> 63.0 us).
 struct TileCost {
   double single, pair, tile;
 };
-constexpr TileCost kCost64x128{0.566, 0.670, 0.357};
-constexpr TileCost kCost128x128{0.627, 0.796, 1.930};
-constexpr TileCost kCost256x256{1.086, 0.0, 9.180};
+constexpr TileCost kCost64x128{0.576, 0.598, 0.0};
+constexpr TileCost kCost128x128{0.616, 0.765, 1.085};
+constexpr TileCost kCost256x256{1.086, 0.0, 7.200};
+constexpr TileCost kCost192x256{0.948, 0.0, 4.843};
+constexpr double kCostLaunch = 1.925;  // the tail plan's second launch
 
 double grid_cost(int tile, int64_t M, int64_t N, int64_t nkt, bool gateup) {
   const int64_t n = tile_count(tile, M, N, gateup);
   if (n == 0) return 0.0;
   const int64_t k = (n + kCUs - 1) / kCUs;
-  const TileCost& c =
-      tile == kT64x128 ? kCost64x128 : (tile == kT128x128 ? kCost128x128 : kCost256x256);
+  const TileCost& c = tile == kT64x128    ? kCost64x128
+                      : tile == kT128x128 ? kCost128x128
+                      : tile == kT192x256 ? kCost192x256
+                                          : kCost256x256;
   if (kTiles[tile].per_cu == 1) return (double)k * ((double)nkt * c.single + c.tile);
   const int64_t pairs = k / 2, singles = k % 2;
   return (double)nkt * ((double)pairs * c.pair + (double)singles * c.single) +
          (double)(pairs + singles) * c.tile;
 }
 
-// The unsplit plan: the cheapest of 64 x 128, 128 x 128, 256 x 256, and
+// The unsplit plan: the cheapest of 64 x 128, 128 x 128, 256 x 256, 192 x 256, and
 // "256 x 256 for whole rounds + a 128 x 128 tail" (nmain > 0: the first
 // nmain output columns as whole 256 x 256 rounds, the rest as 128 x 128 tiles
 // in a second launch). The tail form turns the last partial round of 256 x
@@ -463,7 +470,7 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup) {
   const int64_t nkt = K / kBK;
   GemmPlan best{kT64x128, 0};
   double cbest = grid_cost(kT64x128, M, N, nkt, gateup);
-  for (int t : {kT128x128, kT256x256}) {
+  for (int t : {kT128x128, kT256x256, kT192x256}) {
     const double c = grid_cost(t, M, N, nkt, gateup);
     if (c < cbest) best = GemmPlan{t, 0}, cbest = c;
   }
@@ -474,7 +481,7 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (main_nt > 0 && main_nt < n_nt) {
     const int64_t nmain = main_nt * cols;
     const double c = grid_cost(kT256x256, M, nmain, nkt, gateup) +
-                     grid_cost(kT128x128, M, N - nmain, nkt, gateup);
+                     grid_cost(kT128x128, M, N - nmain, nkt, gateup) + kCostLaunch;
     if (c < cbest) best = GemmPlan{kT256x256, nmain}, cbest = c;
   }
   const auto per_cu = [&](int t) { return (tile_count(t, M, N, gateup) + kCUs - 1) / kCUs; };
@@ -489,6 +496,7 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
   switch (p.tile) {
     case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
     case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
+    case kT192x256: return launch_gemm_cfg<192, 256, 2, 4, GATEUP, 2>(a, s);
     default: break;
   }
   if (p.nmain == 0) return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);

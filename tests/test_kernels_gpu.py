@@ -284,9 +284,10 @@ def test_qwen3_4b_prefill_8192_rows():
     check_ffn(8192, 8192, K, I, label="4B gate-up M=8192 (row subset)")
 
 
-# Row counts whose prefill grids differ on Qwen3-4B shapes: 64 x 128, 128 x 128
-# and 256 x 256 tiles, and whole 256 x 256 rounds followed by a 128 x 128 tail
-# launch (gate-up at 1024 and 2048 rows, QKV at 3072).
+# Row counts whose prefill grids differ on Qwen3-4B shapes: 64 x 128 (gate-up
+# 128 rows, QKV 384), 128 x 128 (gate-up 384, QKV 768), 192 x 256 (gate-up 512,
+# QKV 1536 and 2048) and 256 x 256 tiles (gate-up 1536), and whole 256 x 256
+# rounds followed by a 128 x 128 tail launch (gate-up 1024 and 2048, QKV 3072).
 PLAN_ROWS = {"gate_up": (2048, [128, 384, 512, 1024, 1536]),
              "qkv": (3072, [384, 768, 1536, 2048])}
 
