@@ -60,7 +60,7 @@ int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* gamma, float 
 template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s);
 
-// Split-K bf16 MFMA tiles for the middle regime (fp_splitk.hip): used by
+// Split-K MFMA tiles for the middle regime (fp_splitk.hip). bf16: used by
 // launch_stream from kSplitkMinM rows (kSplitkMinMSmallN for calls with at
 // most kSplitkSmallN weight rows) and by launch_tiled for small-N calls up to
 // kSplitkMaxM rows with K >= kSplitkMinKTiled, when splitk_supported() holds.
@@ -69,8 +69,22 @@ constexpr int64_t kSplitkMinMSmallN = 3;
 constexpr int64_t kSplitkSmallN = 8192;
 constexpr int64_t kSplitkMaxM = 256;
 constexpr int64_t kSplitkMinKTiled = 2048;
-bool splitk_supported(const StreamArgs& a, bool aligned);
-template <bool GATEUP>
+constexpr int64_t kSplitkMaxM8 = 128;
+bool splitk_supported(const StreamArgs& a, bool aligned, bool w8);
+// Whether an int8 call of this shape (M rows, N outputs) runs the split-K
+// tiles (dequantising in registers) rather than the row, streaming or
+// dequantise-first paths. Measured on MI355X over Qwen3-4B/8B QKV, gate-up,
+// o and down: from 2 rows for gate-up and 3 for other outputs (5 for outputs
+// of at most 4096 columns with K <= 8192, where the row kernel holds up to
+// 4), up to 128 rows; above 64 rows only with K <= 8192 (the long-K down
+// projections keep the dequantise-first path with k split across
+// workgroups).
+inline bool splitk8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
+  const int64_t min_m = gateup ? 2 : ((N <= 4096 && K <= 8192) ? 5 : 3);
+  if (M < min_m || M > kSplitkMaxM8 || K % 64 != 0) return false;
+  return M <= 64 || K <= 8192;
+}
+template <bool GATEUP, bool W8>
 int launch_splitk(const StreamArgs& a, hipStream_t s);
 
 // Direct-to-LDS bf16 MFMA contraction (fp_gemm.hip), used by launch_tiled

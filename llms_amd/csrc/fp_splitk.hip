@@ -14,8 +14,11 @@
 // waves' partial tiles are summed through LDS in fixed wave order and the
 // epilogue (bf16 store, or silu(g)*u at torch's rounding points) runs on
 // wave 0's share of the tile.
-// Requirements (checked by splitk_supported): bf16, K % 64 == 0,
-// 16-byte-aligned rows, operand byte sizes below 2^31.
+// int8 weights (W8) land in LDS as int8 (64 B per row and k-step) and each
+// lane dequantises its MFMA A fragment in registers to bf16(q * s), exactly
+// as the dequantise-then-matmul path rounds it.
+// Requirements (checked by splitk_supported): K % 64 == 0, 16-byte-aligned
+// rows, operand byte sizes below 2^31, int8 row scales present.
 #include "fp_common.h"
 #include "fp_launch.h"
 
@@ -30,6 +33,7 @@ constexpr int kRPI = 1024 / (kBK * 2);   // tile rows per load instruction
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & (kCPR - 1); }
+__device__ __forceinline__ int swz8(int r) { return (r >> 2) & 3; }
 
 // buffer_load_dwordx4 ... lds: 16 bytes per lane from base + voff + soff into
 // LDS at dst + 16 * lane; bytes at or past `nbytes` read as zero.
@@ -44,23 +48,28 @@ __device__ __forceinline__ void load_lds16(const void* base, int nbytes, lds_ptr
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= v only.
 constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >> 4) << 14); }
 
-template <int BN, int BM, int NW, int NS, bool GATEUP>
+template <int BN, int BM, int NW, int NS, bool GATEUP, bool W8>
 __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_mt) {
-  constexpr int FN = BN / 16, FM = BM / 16;  // MFMA sub-tiles (the whole tile per wave)
-  constexpr int IW = BN / kRPI, IX = BM / kRPI;  // load instructions per stage
+  constexpr int WB = W8 ? 1 : 2;               // bytes per weight element
+  constexpr int WROW = kBK * WB;               // bytes of a weight tile row per step
+  constexpr int WRPI = 1024 / WROW;            // weight rows per load instruction
+  constexpr int WCPR = WROW / 16;              // 16-byte chunks per weight row
+  constexpr int FN = BN / 16, FM = BM / 16;    // MFMA sub-tiles (the whole tile per wave)
+  constexpr int IW = BN / WRPI, IX = BM / kRPI;  // load instructions per stage
   constexpr int kPerStep = IW + IX;
-  static_assert(BN % 16 == 0 && BM % 16 == 0, "tile");
+  constexpr int SW = BN * WROW, SX = BM * kBK * 2;  // bytes per wave and stage
+  static_assert(BN % 16 == 0 && BM % 16 == 0 && BN % WRPI == 0, "tile");
   static_assert(!GATEUP || BN % 32 == 0, "gate-up tiles hold whole gate/up 16-row pairs");
   static_assert(NS == 2 || NS == 3, "LDS stages");
   // the partial tiles of waves 1 .. NW-1 are summed in stage 0's space
-  static_assert((NW - 1) * FN * FM * 256 * 4 <= NW * (BN + BM) * kBK * 2, "reduction space");
+  static_assert((NW - 1) * FN * FM * 256 * 4 <= NW * (SW + SX), "reduction space");
 
   // One LDS object per stage (distinct alias scopes: reads of one stage are
   // not ordered after the asynchronous writes into another), each split per
-  // wave into W rows then x rows.
-  __shared__ __attribute__((aligned(1024))) uint16_t sS0[NW][BN + BM][kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sS1[NW][BN + BM][kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sS2[NS > 2 ? NW : 1][BN + BM][kBK];
+  // wave into the weight rows (SW bytes) then the x rows (SX bytes).
+  __shared__ __attribute__((aligned(1024))) char sS0[NW][SW + SX];
+  __shared__ __attribute__((aligned(1024))) char sS1[NW][SW + SX];
+  __shared__ __attribute__((aligned(1024))) char sS2[NS > 2 ? NW : 1][SW + SX];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -70,43 +79,64 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
   const int64_t m0 = (int64_t)tm * BM;
   const int64_t c0 = (int64_t)tn * (GATEUP ? BN / 2 : BN);  // first output column
 
+  // Weight row t of the tile: output n(t) of matrix Wu when up(t) (gate-up
+  // tiles interleave 16-row groups of Wg and Wu).
+  auto wrow_n = [&](int t) -> int64_t { return GATEUP ? c0 + (t / 32) * 16 + (t % 16) : c0 + t; };
+  auto wrow_up = [&](int t) -> bool { return GATEUP && ((t / 16) & 1); };
+
   // Per-lane byte offsets of this lane's 16 B in each load instruction (see
-  // fp_gemm.hip: instruction q fills tile rows 8q .. 8q+7, the swizzle is
-  // applied on the global side so the LDS writes stay lane-linear).
+  // fp_gemm.hip: a load instruction fills 1 KB of consecutive tile rows; the
+  // swizzle is applied on the global side so the LDS writes stay
+  // lane-linear). bf16 weight rows (128 B per step): chunk c of row r at
+  // c ^ ((r >> 1) & 7); int8 rows (64 B per step): c ^ ((r >> 2) & 3), which
+  // keeps the 8-byte fragment reads of 16 rows on distinct banks.
   const int lrow = lane / kCPR, lchunk = lane % kCPR;
   uint32_t woff[IW];
 #pragma unroll
   for (int q = 0; q < IW; ++q) {
-    const int t = q * kRPI + lrow;
-    const int64_t n = GATEUP ? c0 + (t / 32) * 16 + (t % 16) : c0 + t;
-    const int64_t ld = (GATEUP && ((t / 16) & 1)) ? a.ldw1 : a.ldw0;
-    woff[q] = (uint32_t)(n * ld * 2) + (uint32_t)((lchunk ^ swz(t)) * 16);
+    const int t = q * WRPI + lane / WCPR;
+    const int c = lane % WCPR;
+    const int64_t ld = wrow_up(t) ? a.ldw1 : a.ldw0;
+    woff[q] = (uint32_t)(wrow_n(t) * ld * WB) + (uint32_t)((c ^ (W8 ? swz8(t) : swz(t))) * 16);
   }
   uint32_t xoff[IX];
 #pragma unroll
   for (int q = 0; q < IX; ++q) {
     const int t = q * kRPI + lrow;
-    xoff[q] = (uint32_t)((m0 + t) * a.ldx * 2) + (uint32_t)((lchunk ^ swz(BN + t)) * 16);
+    xoff[q] = (uint32_t)((m0 + t) * a.ldx * 2) + (uint32_t)((lchunk ^ swz(t)) * 16);
   }
-  const int wbytes0 = (int)((a.N - 1) * a.ldw0 * 2 + a.K * 2);
-  const int wbytes1 = GATEUP ? (int)((a.N - 1) * a.ldw1 * 2 + a.K * 2) : wbytes0;
+  const int wbytes0 = (int)((a.N - 1) * a.ldw0 * WB + a.K * WB);
+  const int wbytes1 = GATEUP ? (int)((a.N - 1) * a.ldw1 * WB + a.K * WB) : wbytes0;
   const int xbytes = (int)((a.M - 1) * a.ldx * 2 + a.K * 2);
   void* const wptr1 = (void*)(GATEUP ? a.w1 : a.w0);
 
-  auto stage = [&](int s) -> uint16_t (*)[kBK] {
+  // int8: this lane's row scales (rows 16 i + li), zero past N
+  float sc[W8 ? FN : 1], nsc[W8 ? FN : 1];
+  if constexpr (W8) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int t = 16 * i + li;
+      const int64_t n = wrow_n(t);
+      sc[i] = n < a.N ? (wrow_up(t) ? a.s1 : a.s0)[n] : 0.f;
+      nsc[i] = -128.f * sc[i];
+    }
+  }
+
+  auto stage = [&](int s) -> char* {
     return s == 0 ? sS0[wave] : (s == 1 ? sS1[wave] : sS2[NS > 2 ? wave : 0]);
   };
   auto issue = [&](int s, int64_t k0) {
-    uint16_t (*t)[kBK] = stage(s);
-    const uint32_t kb = (uint32_t)(k0 * 2);
+    char* t = stage(s);
 #pragma unroll
     for (int q = 0; q < IW; ++q) {
-      const bool up = GATEUP && ((q / 2) & 1);  // 16-row groups alternate Wg, Wu
-      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0, (lds_ptr_t)&t[q * kRPI][0], woff[q], kb);
+      // instruction q holds 16-row groups of one matrix (uniform per instruction)
+      const bool up = wrow_up(q * WRPI);
+      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0, (lds_ptr_t)(t + q * 1024), woff[q],
+                 (uint32_t)(k0 * WB));
     }
 #pragma unroll
     for (int q = 0; q < IX; ++q)
-      load_lds16(a.x, xbytes, (lds_ptr_t)&t[BN + q * kRPI][0], xoff[q], kb);
+      load_lds16(a.x, xbytes, (lds_ptr_t)(t + SW + q * 1024), xoff[q], (uint32_t)(k0 * 2));
   };
 
   f32x4 acc[FN][FM];
@@ -115,17 +145,26 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // fragment byte offsets (swz of row 16 i + li does not depend on i)
-  const uint32_t offa = (uint32_t)(li * kBK * 2 + ((grp ^ swz(li)) * 16));
-  const uint32_t offb = (uint32_t)((BN + li) * kBK * 2 + ((grp ^ swz(BN + li)) * 16));
+  // fragment byte offsets (the swizzle of row 16 i + li does not depend on
+  // i). k-substep kk: bf16 flips chunk bit 2, int8 chunk bit 1.
+  const uint32_t offa = W8 ? (uint32_t)(li * WROW + ((((grp >> 1) ^ swz8(li)) * 16) | ((grp & 1) * 8)))
+                           : (uint32_t)(li * WROW + ((grp ^ swz(li)) * 16));
+  const uint32_t offb = (uint32_t)(SW + li * kBK * 2 + ((grp ^ swz(li)) * 16));
   auto compute = [&](int s) {
-    const char* t = (const char*)stage(s);
+    const char* t = stage(s);
 #pragma unroll
     for (int kk = 0; kk < kBK / 32; ++kk) {
-      const uint32_t oa = offa ^ (uint32_t)(kk * 64), ob = offb ^ (uint32_t)(kk * 64);
+      const uint32_t oa = offa ^ (uint32_t)(kk * (W8 ? 32 : 64)), ob = offb ^ (uint32_t)(kk * 64);
       u32x4 fa[FN], fb[FM];
 #pragma unroll
-      for (int i = 0; i < FN; ++i) fa[i] = *reinterpret_cast<const u32x4*>(t + oa + i * 16 * kBK * 2);
+      for (int i = 0; i < FN; ++i) {
+        if constexpr (W8) {
+          const u32x2 q = *reinterpret_cast<const u32x2*>(t + oa + i * 16 * WROW);
+          fa[i] = dequant8_bf16(q.x, q.y, sc[i], nsc[i]);
+        } else {
+          fa[i] = *reinterpret_cast<const u32x4*>(t + oa + i * 16 * WROW);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < FM; ++j) fb[j] = *reinterpret_cast<const u32x4*>(t + ob + j * 16 * kBK * 2);
 #pragma unroll
@@ -158,7 +197,7 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
   }
 
   // Fixed-order cross-wave sum through LDS (the ring is free now).
-  float* red = reinterpret_cast<float*>(&sS0[0][0][0]);
+  float* red = reinterpret_cast<float*>(&sS0[0][0]);
   __syncthreads();
   if (wave > 0) {
 #pragma unroll
@@ -207,12 +246,12 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
   }
 }
 
-template <int BN, int BM, int NW, int NS, bool GATEUP>
+template <int BN, int BM, int NW, int NS, bool GATEUP, bool W8>
 int launch_splitk_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t cols = GATEUP ? BN / 2 : BN;
   const int n_nt = (int)((a.N + cols - 1) / cols);
   const int n_mt = (int)((a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((splitk_kernel<BN, BM, NW, NS, GATEUP>), dim3((unsigned)(n_nt * n_mt)),
+  hipLaunchKernelGGL((splitk_kernel<BN, BM, NW, NS, GATEUP, W8>), dim3((unsigned)(n_nt * n_mt)),
                      dim3(NW * kWave), 0, s, a, n_mt);
   return (int)hipGetLastError();
 }
@@ -220,35 +259,50 @@ int launch_splitk_cfg(const StreamArgs& a, hipStream_t s) {
 }  // namespace
 
 #ifndef FP_SPLITK_NO_DISPATCH
-bool splitk_supported(const StreamArgs& a, bool aligned) {
+bool splitk_supported(const StreamArgs& a, bool aligned, bool w8) {
   constexpr int64_t kLim = (int64_t)1 << 31;
+  const int64_t wb = w8 ? 1 : 2;
   if (!aligned || a.K % kBK != 0) return false;
-  if ((a.N - 1) * a.ldw0 * 2 + a.K * 2 >= kLim) return false;
-  if (a.w1 && (a.N - 1) * a.ldw1 * 2 + a.K * 2 >= kLim) return false;
+  if (w8 && (!a.s0 || (a.w1 && !a.s1))) return false;
+  if ((a.N - 1) * a.ldw0 * wb + a.K * wb >= kLim) return false;
+  if (a.w1 && (a.N - 1) * a.ldw1 * wb + a.K * wb >= kLim) return false;
   if ((a.M - 1) * a.ldx * 2 + a.K * 2 >= kLim) return false;
   return true;
 }
 
-// Tile table measured on MI355X (Qwen3-4B and -8B shapes, 12 cycled weight
-// sets): the x tile is M rounded up to 16 (up to 64 rows), then 64 x 64
-// tiles; gate-up tiles hold 16 outputs (32 weight rows).
-template <bool GATEUP>
+// Tile tables measured on MI355X (Qwen3-4B and -8B shapes, cycled weight
+// sets, warm clocks): the x tile is M rounded up to 16 (up to 64 rows), then
+// 64 x 64 tiles; gate-up tiles hold 16 outputs (32 weight rows). int8 (half
+// the bytes per weight row, so more rows of LDS per wave) prefers 8 waves.
+template <bool GATEUP, bool W8>
 int launch_splitk(const StreamArgs& a, hipStream_t s) {
-  if constexpr (GATEUP) {
-    if (a.M <= 16) return launch_splitk_cfg<32, 16, 4, 3, true>(a, s);
-    if (a.M <= 32) return launch_splitk_cfg<32, 32, 8, 2, true>(a, s);
-    if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, true>(a, s);
-    return launch_splitk_cfg<64, 64, 4, 2, true>(a, s);
+  if constexpr (W8 && GATEUP) {
+    if (a.M <= 16) return launch_splitk_cfg<32, 16, 8, 2, true, true>(a, s);
+    if (a.M <= 32) return launch_splitk_cfg<32, 32, 4, 3, true, true>(a, s);
+    if (a.M <= 64) return launch_splitk_cfg<32, 64, 8, 2, true, true>(a, s);
+    return launch_splitk_cfg<64, 64, 4, 2, true, true>(a, s);
+  } else if constexpr (W8) {
+    if (a.M <= 16) return launch_splitk_cfg<32, 16, 8, 3, false, true>(a, s);
+    if (a.M <= 32) return launch_splitk_cfg<32, 32, 8, 2, false, true>(a, s);
+    if (a.M <= 64) return launch_splitk_cfg<32, 64, 8, 2, false, true>(a, s);
+    return launch_splitk_cfg<64, 64, 4, 2, false, true>(a, s);
+  } else if constexpr (GATEUP) {
+    if (a.M <= 16) return launch_splitk_cfg<32, 16, 4, 3, true, W8>(a, s);
+    if (a.M <= 32) return launch_splitk_cfg<32, 32, 8, 2, true, W8>(a, s);
+    if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, true, W8>(a, s);
+    return launch_splitk_cfg<64, 64, 4, 2, true, W8>(a, s);
   } else {
-    if (a.M <= 16) return launch_splitk_cfg<16, 16, 4, 3, false>(a, s);
-    if (a.M <= 32) return launch_splitk_cfg<32, 32, 4, 3, false>(a, s);
-    if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, false>(a, s);
-    return launch_splitk_cfg<64, 64, 4, 2, false>(a, s);
+    if (a.M <= 16) return launch_splitk_cfg<16, 16, 4, 3, false, W8>(a, s);
+    if (a.M <= 32) return launch_splitk_cfg<32, 32, 4, 3, false, W8>(a, s);
+    if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, false, W8>(a, s);
+    return launch_splitk_cfg<64, 64, 4, 2, false, W8>(a, s);
   }
 }
 
-template int launch_splitk<false>(const StreamArgs&, hipStream_t);
-template int launch_splitk<true>(const StreamArgs&, hipStream_t);
+template int launch_splitk<false, false>(const StreamArgs&, hipStream_t);
+template int launch_splitk<true, false>(const StreamArgs&, hipStream_t);
+template int launch_splitk<false, true>(const StreamArgs&, hipStream_t);
+template int launch_splitk<true, true>(const StreamArgs&, hipStream_t);
 #endif
 
 }  // namespace fp

@@ -350,6 +350,9 @@ int launch_stream_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // QKV 2 (QKV's 3x smaller grid is latency-bound and prefers occupancy).
 template <bool GATEUP, bool W8>
 int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
+  // int8 from a few rows: split-K tiles dequantising in registers (fp_splitk.hip)
+  if (W8 && splitk8_shape(a.M, a.N, a.K, GATEUP) && splitk_supported(a, aligned, true))
+    return launch_splitk<GATEUP, true>(a, s);
   // one or a few rows: contiguous row streaming (fp_rows.hip)
   if (rows_supported<W8>(a, aligned)) return launch_rows<GATEUP, W8>(a, s);
   // bf16 against large weights with a caller workspace: k split across
@@ -359,7 +362,8 @@ int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
   // bf16 from 3 (small N, e.g. QKV) or 8 rows: split-K tiles (fp_splitk.hip)
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
   const int64_t min_m = wrows <= kSplitkSmallN ? kSplitkMinMSmallN : kSplitkMinM;
-  if (!W8 && a.M >= min_m && splitk_supported(a, aligned)) return launch_splitk<GATEUP>(a, s);
+  if (!W8 && a.M >= min_m && splitk_supported(a, aligned, false))
+    return launch_splitk<GATEUP, false>(a, s);
   // (int8 dequantisation needs registers of its own: 2 k-blocks per buffer)
   constexpr int U8 = (GATEUP && !W8) ? 4 : 2;
   if (a.M <= 8) return launch_stream_cfg<4, 1, U8, 0, GATEUP, W8, false, true>(a, aligned, s);

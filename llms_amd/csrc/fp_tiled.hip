@@ -211,17 +211,21 @@ int launch_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // the caller gave a workspace, else unsplit — except, without the split, up
 // to kSplitkMaxM rows against at most 8192 weight rows with K >=
 // kSplitkMinKTiled (Qwen3-4B QKV: 6144 x 2560), which give too few tiles for
-// 256 CUs and run the in-workgroup split-K tiles. int8, unaligned rows and K
-// tails run tiled_kernel.
+// 256 CUs and run the in-workgroup split-K tiles. int8 shapes that
+// splitk8_shape() admits run the split-K tiles too (in-register
+// dequantisation); other int8 calls, unaligned rows and K tails run
+// tiled_kernel.
 template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
   GemmSplit sp;
   if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP>(a, sp, s);
   if (!W8 && a.M <= kSplitkMaxM && wrows <= kSplitkSmallN && a.K >= kSplitkMinKTiled &&
-      splitk_supported(a, aligned))
-    return launch_splitk<GATEUP>(a, s);
+      splitk_supported(a, aligned, false))
+    return launch_splitk<GATEUP, false>(a, s);
   if (!W8 && gemm_supported(a, aligned)) return launch_gemm<GATEUP>(a, s);
+  if (W8 && splitk8_shape(a.M, a.N, a.K, GATEUP) && splitk_supported(a, aligned, true))
+    return launch_splitk<GATEUP, true>(a, s);
   return launch_cfg<128, 128, 64, 2, 2, GATEUP, W8>(a, aligned, s);
 }
 

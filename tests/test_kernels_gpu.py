@@ -395,13 +395,14 @@ def test_qwen3_4b_int8(M):
     _check(y[rows], out, f"4B int8 gate-up M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 4, 100])
+@pytest.mark.parametrize("M", [1, 4, 16, 100])
 def test_int8_dequant_bit_exact(M):
     """In-register dequantisation is bit-exact: with one-hot x rows the QKV
     output is a single dequantised weight, y[m, n] = bf16(q[n, k_m] * s[n])
     (a one-term sum is exact, then rounded to bf16, which it already is), so it
     must equal the oracle's dequant_w8 column bit for bit — through the row
-    kernel (M = 1), the streaming kernel (M = 4) and the tiled one (M = 100)."""
+    kernel (M = 1 and 4 on this 384-output shape) and the split-K tiles (M = 16
+    from the streaming dispatch, M = 100 from the tiled one)."""
     K, N = 2560, 384
     _, w = qkv_inputs(70 + M, 1, K, N - 128, 64, w_std=0.05)
     q, s = _quant(w)
@@ -412,6 +413,39 @@ def test_int8_dequant_bit_exact(M):
     yq, yk, yv = _kernels().fused_qkv_w8(x.to(DEV), q, s, n_q=N - 128, n_k=64)
     y = bits(torch.cat([yq, yk, yv], -1).cpu())
     np.testing.assert_array_equal(y, deq[:, ks].T)
+
+
+@pytest.mark.parametrize("M", [2, 3, 16, 33, 64, 100, 128])
+def test_int8_split_k_tiles(M):
+    """The int8 split-K tiles (weights land in LDS as int8, each lane
+    dequantises its MFMA fragment): gate-up, QKV and the plain projection with
+    output counts that leave partial tiles, an all-zero weight row, and for the
+    projection both a short K (split-K from 5 rows) and a long K (split-K up to
+    64 rows, the dequantise-first path above)."""
+    kern = _kernels()
+    K = 2048
+    x, wg, wu = ffn_inputs(500 + M, M, K, 1000)
+    wg[7] = 0
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+    _check(y, ref.ref_gate_up_silu_w8_full(bits(x), qg.cpu().numpy(), sg.cpu().numpy(),
+                                           qu.cpu().numpy(), su.cpu().numpy()),
+           f"int8 split-K gate-up M={M} N=1000")
+    n_q, n_k = 256, 72
+    x, w = qkv_inputs(510 + M, M, K, n_q, n_k)
+    w[5] = 0
+    q, s = _quant(w)
+    yq, yk, yv = kern.fused_qkv_w8(x.to(DEV), q, s, n_q=n_q, n_k=n_k)
+    _check(torch.cat([yq, yk, yv], -1).cpu(),
+           ref.ref_qkv_w8_full(bits(x), q.cpu().numpy(), s.cpu().numpy(), n_q, n_k),
+           f"int8 split-K qkv M={M} N={n_q + 2 * n_k}")
+    for Kl, N in ((4096, 300), (9728, 264)):
+        x, w = qkv_inputs(520 + M + Kl, M, Kl, N, 0)
+        q, s = _quant(w)
+        y = kern.fused_linear_w8(x.to(DEV), q, s).cpu()
+        _check(y, ref.ref_linear_w8(bits(x), q.cpu().numpy(), s.cpu().numpy()),
+               f"int8 linear M={M} K={Kl} N={N}")
 
 
 def test_int8_tails_and_zero_rows():
@@ -518,17 +552,21 @@ def test_split_k_across_workgroups(M, N, K, op):
     _check(y.cpu()[rows], ref.ref_linear(bits(x)[rows], bits(w)), f"split {op} M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("M,K,N,op,dq", [(47, 2560, 6144, "qkv", False), (48, 2560, 6144, "qkv", True),
+@pytest.mark.parametrize("M,K,N,op,dq", [(47, 2576, 6144, "qkv", False), (48, 2576, 6144, "qkv", True),
+                                         (48, 2560, 6144, "qkv", False),
                                          (64, 1040, 1001, "gate-up", True),
                                          (200, 1040, 1001, "gate-up", False),
                                          (256, 1040, 1001, "gate-up", True),
+                                         (128, 9728, 2560, "linear", True),
+                                         (128, 4096, 2560, "linear", False),
                                          (512, 9728, 2560, "linear", True),
                                          (300, 2560, 9728, "gate-up", True)])
 def test_int8_dequantised_mfma_path(M, K, N, op, dq):
     """With enough rows the int8 calls dequantise the weights into the
     workspace and run the bf16 path (split across workgroups where planned);
-    the contract is unchanged. Below the threshold the in-register int8
-    kernels run."""
+    the contract is unchanged. Below the threshold, and where the int8 split-K
+    tiles take the shape (K % 64 == 0, up to 128 rows, K <= 8192 above 64),
+    the in-register int8 kernels run."""
     from llms_amd import _lib
 
     gu = op == "gate-up"
