@@ -86,7 +86,8 @@ inline int64_t dequant_bytes(int64_t N, int64_t K, bool gateup) {
 
 inline bool use_dequant(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (K % 16 != 0 || M < 48) return false;
-  if (splitk8_shape(M, N, K, gateup)) return false;  // the int8 split-K tiles take these
+  // the int8 split-K tiles and the int8 gemm take these
+  if (splitk8_shape(M, N, K, gateup) || gemm8_shape(M, N, K, gateup)) return false;
   if (!gateup || M <= kStreamMaxM) return true;
   return M >= (2 * N * K > ((int64_t)1 << 26) ? 512 : 256);
 }

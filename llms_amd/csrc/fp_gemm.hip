@@ -35,6 +35,7 @@ constexpr int kGroupM = 8;       // m-tiles per group of the tile order
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & (kCPR - 1); }
+__device__ __forceinline__ int swz8(int r) { return (r >> 2) & 3; }
 
 // buffer_load_dwordx4 ... lds: 16 bytes per lane from base + voff + soff into
 // LDS at dst + 16 * lane; bytes at or past `nbytes` read as zero.
@@ -54,15 +55,29 @@ constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >>
 // contiguous range of k-steps, and the fp32 accumulators go to the workspace
 // ws[split][m][col] (col: output column n; gate-up: g at n, u at N + n) for
 // splitk_reduce_kernel, which sums them in split order.
-template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool SPLIT = false>
+// W8: int8 weights with per-row scales (a.s0, a.s1). A weight tile row is 64 B
+// per k-step in LDS (16 rows per load instruction, chunk c of row r at
+// c ^ ((r >> 2) & 3)); each lane turns the 8 int8 of its MFMA A fragment into
+// bf16(q * s) in registers (dequant8_bf16: the dequantise-then-matmul
+// rounding) before the bf16 MFMA.
+template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool SPLIT = false, bool W8 = false>
 __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int n_mt, int n_nt,
                                                               int ksteps, float* ws) {
   constexpr int NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;   // per-wave tile
   constexpr int FN = TN / 16, FM = TM / 16;   // MFMA sub-tiles per wave
-  constexpr int IW = BN / kRPI / NW;          // weight load instructions per wave per stage
+  constexpr int WB = W8 ? 1 : 2;              // bytes per weight element
+  constexpr int WKE = kBK * WB / 2;           // weight LDS row, in 16-bit units
+  constexpr int WRPI = W8 ? 16 : kRPI;        // weight rows per load instruction
+  constexpr int WCPR = W8 ? 4 : kCPR;         // 16-byte chunks per weight row
+  constexpr int NWI = BN / WRPI;              // weight load instructions per stage
+  constexpr int IW = (NWI + NW - 1) / NW;     // ... per wave (the last may be idle)
   constexpr int IX = BM / kRPI / NW;          // x load instructions per wave per stage
-  static_assert(BN % (kRPI * NW) == 0 && BM % (kRPI * NW) == 0, "tile/waves");
+  static_assert(BN % WRPI == 0 && BM % (kRPI * NW) == 0, "tile/waves");
+  static_assert(W8 || NWI % NW == 0, "bf16 weight loads spread evenly over the waves");
+  // with three stages the waits count a wave's loads per step, so they must
+  // be the same for every wave
+  static_assert(NS == 2 || NWI % NW == 0, "three stages need even weight loads");
   static_assert(!GATEUP || TN % 32 == 0, "gate-up needs whole gate/up pairs per wave");
   static_assert(NS == 2 || NS == 3, "LDS stages");
 
@@ -70,9 +85,9 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   // alias scopes, so the compiler can see that fragment reads of one stage do
   // not depend on the asynchronous global->LDS writes into another stage
   // (with a single [NS][..] array it waits for all loads before every read).
-  __shared__ __attribute__((aligned(1024))) uint16_t sW0[BN][kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sW1[BN][kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sW2[NS > 2 ? BN : 1][kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sW0[BN][WKE];
+  __shared__ __attribute__((aligned(1024))) uint16_t sW1[BN][WKE];
+  __shared__ __attribute__((aligned(1024))) uint16_t sW2[NS > 2 ? BN : 1][WKE];
   __shared__ __attribute__((aligned(1024))) uint16_t sX0[BM][kBK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX1[BM][kBK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX2[NS > 2 ? BM : 1][kBK];
@@ -109,14 +124,18 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   // sizes below 2^32.
   const int lrow = lane / kCPR;                 // row within an instruction's 8
   const int lchunk = lane % kCPR;               // LDS chunk position it fills
+  // weight tile row t: output n(t) of matrix Wu when up(t) (gate-up tiles
+  // interleave 16-row groups of Wg and Wu)
+  auto wrow_n = [&](int t) -> int64_t { return GATEUP ? c0 + (t / 32) * 16 + (t % 16) : c0 + t; };
+  auto wrow_up = [&](int t) -> bool { return GATEUP && ((t / 16) & 1); };
   uint32_t woff[IW];
 #pragma unroll
   for (int j = 0; j < IW; ++j) {
     const int q = wave + NW * j;
-    const int t = q * kRPI + lrow;
-    const int64_t n = GATEUP ? c0 + (t / 32) * 16 + (t % 16) : c0 + t;
-    const int64_t ld = (GATEUP && ((t / 16) & 1)) ? a.ldw1 : a.ldw0;
-    woff[j] = (uint32_t)(n * ld * 2) + (uint32_t)((lchunk ^ swz(t)) * 16);
+    const int t = q * WRPI + lane / WCPR;
+    const int c = lane % WCPR;
+    const int64_t ld = wrow_up(t) ? a.ldw1 : a.ldw0;
+    woff[j] = (uint32_t)(wrow_n(t) * ld * WB) + (uint32_t)((c ^ (W8 ? swz8(t) : swz(t))) * 16);
   }
   uint32_t xoff[IX];
 #pragma unroll
@@ -125,20 +144,33 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
     xoff[j] = (uint32_t)((m0 + t) * a.ldx * 2) + (uint32_t)((lchunk ^ swz(t)) * 16);
   }
   // byte sizes of the buffer resources (rows past them read as zeros)
-  const int wbytes0 = (int)((a.N - 1) * a.ldw0 * 2 + a.K * 2);
-  const int wbytes1 = GATEUP ? (int)((a.N - 1) * a.ldw1 * 2 + a.K * 2) : wbytes0;
+  const int wbytes0 = (int)((a.N - 1) * a.ldw0 * WB + a.K * WB);
+  const int wbytes1 = GATEUP ? (int)((a.N - 1) * a.ldw1 * WB + a.K * WB) : wbytes0;
   const int xbytes = (int)((a.M - 1) * a.ldx * 2 + a.K * 2);
   void* const wptr1 = (void*)(GATEUP ? a.w1 : a.w0);
 
-  auto issue = [&](uint16_t (*tw)[kBK], uint16_t (*tx)[kBK], int64_t k0) {
+  // int8: this lane's row scales (weight rows wn * TN + 16 i + li), zero past N
+  float sc[W8 ? FN : 1], nsc[W8 ? FN : 1];
+  if constexpr (W8) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int t = wn * TN + 16 * i + li;
+      const int64_t n = wrow_n(t);
+      sc[i] = n < a.N ? (wrow_up(t) ? a.s1 : a.s0)[n] : 0.f;
+      nsc[i] = -128.f * sc[i];
+    }
+  }
+
+  auto issue = [&](uint16_t (*tw)[WKE], uint16_t (*tx)[kBK], int64_t k0) {
     const uint32_t kb = (uint32_t)(k0 * 2);
 #pragma unroll
     for (int j = 0; j < IW; ++j) {
       const int q = wave + NW * j;
+      if (q >= NWI) break;  // uniform per wave
       // gate-up: 16-row groups alternate Wg, Wu; uniform per instruction
-      const bool up = GATEUP && ((q / 2) & 1);
-      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0, (lds_ptr_t)&tw[q * kRPI][0], woff[j],
-                 kb);
+      const bool up = wrow_up(q * WRPI);
+      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0, (lds_ptr_t)&tw[q * WRPI][0], woff[j],
+                 (uint32_t)(k0 * WB));
     }
 #pragma unroll
     for (int j = 0; j < IX; ++j)
@@ -157,16 +189,26 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   // plus the compile-time constants 16 i * 128 and the stage base. k-substep
   // kk = 1 flips chunk bit 2 (chunk (4 + grp) ^ s = (grp ^ s) ^ 4).
   const int ra = wn * TN + li, rb = wm * TM + li;
-  const uint32_t offa = (uint32_t)(ra * kBK * 2 + ((grp ^ swz(ra)) * 16));
+  // int8: 8 bytes at chunk 2 kk + (grp >> 1), half grp & 1 (k-substep kk
+  // flips chunk bit 1)
+  const uint32_t offa =
+      W8 ? (uint32_t)(ra * kBK + ((((grp >> 1) ^ swz8(ra)) * 16) | ((grp & 1) * 8)))
+         : (uint32_t)(ra * kBK * 2 + ((grp ^ swz(ra)) * 16));
   const uint32_t offb = (uint32_t)(rb * kBK * 2 + ((grp ^ swz(rb)) * 16));
-  auto compute = [&](const uint16_t (*tw)[kBK], const uint16_t (*tx)[kBK]) {
+  auto compute = [&](const uint16_t (*tw)[WKE], const uint16_t (*tx)[kBK]) {
 #pragma unroll
     for (int kk = 0; kk < kBK / 32; ++kk) {
-      const uint32_t oa = offa ^ (uint32_t)(kk * 64), ob = offb ^ (uint32_t)(kk * 64);
+      const uint32_t oa = offa ^ (uint32_t)(kk * (W8 ? 32 : 64)), ob = offb ^ (uint32_t)(kk * 64);
       u32x4 fa[FN], fb[FM];
 #pragma unroll
-      for (int i = 0; i < FN; ++i)
-        fa[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * kBK * 2);
+      for (int i = 0; i < FN; ++i) {
+        if constexpr (W8) {
+          const u32x2 q = *reinterpret_cast<const u32x2*>((const char*)tw + oa + i * 16 * kBK);
+          fa[i] = dequant8_bf16(q.x, q.y, sc[i], nsc[i]);
+        } else {
+          fa[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * kBK * 2);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < FM; ++j)
         fb[j] = *reinterpret_cast<const u32x4*>((const char*)tx + ob + j * 16 * kBK * 2);
@@ -179,14 +221,14 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  auto stw = [&](int s) -> uint16_t (*)[kBK] { return s == 0 ? sW0 : (s == 1 ? sW1 : sW2); };
+  auto stw = [&](int s) -> uint16_t (*)[WKE] { return s == 0 ? sW0 : (s == 1 ? sW1 : sW2); };
   auto stx = [&](int s) -> uint16_t (*)[kBK] { return s == 0 ? sX0 : (s == 1 ? sX1 : sX2); };
 
   // Ring of NS stages: k-step k lives in stage k % NS, and while step k is
   // consumed steps k+1 .. k+NS-1 are in flight. After a step, wait until this
   // wave's loads of step k+1 have landed (the NS-2 later steps may stay in
   // flight), then for every wave's.
-  constexpr int kPerStep = IW + IX;  // load instructions per wave per step
+  constexpr int kPerStep = IW + IX;  // load instructions per wave per step (even loads)
   const int64_t kfirst = (int64_t)ks * ksteps;  // first k-step of this workgroup
   const int64_t nleft = a.K / kBK - kfirst;
   const int64_t nkt = SPLIT ? (ksteps < nleft ? (int64_t)ksteps : nleft) : a.K / kBK;
@@ -330,12 +372,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int
 
 }  // namespace
 
-template <int BN, int BM, int WN, int WM, bool GATEUP, int NS>
+template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool W8 = false>
 int launch_gemm_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t cols = GATEUP ? BN / 2 : BN;
   const int n_nt = (int)((a.N + cols - 1) / cols);
   const int n_mt = (int)((a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm_kernel<BN, BM, WN, WM, GATEUP, NS>), dim3((unsigned)(n_nt * n_mt)),
+  hipLaunchKernelGGL((gemm_kernel<BN, BM, WN, WM, GATEUP, NS, false, W8>), dim3((unsigned)(n_nt * n_mt)),
                      dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt, 0, (float*)nullptr);
   return (int)hipGetLastError();
 }
@@ -376,14 +418,16 @@ int launch_gemm_splitk_cfg(const StreamArgs& a, int nsplit, float* ws, hipStream
 }
 
 #ifndef FP_GEMM_NO_DISPATCH
-// Whether gemm_kernel can run this call: bf16 fast path, whole 64-wide
-// k-steps, and every operand's byte size below 2^31 (buffer-resource sizes
-// and 32-bit lane offsets).
-bool gemm_supported(const StreamArgs& a, bool aligned) {
+// Whether gemm_kernel can run this call: whole 64-wide k-steps, 16-byte
+// aligned rows, every operand's byte size below 2^31 (buffer-resource sizes
+// and 32-bit lane offsets); int8 also needs its row scales.
+bool gemm_supported(const StreamArgs& a, bool aligned, bool w8) {
   constexpr int64_t kLim = (int64_t)1 << 31;
+  const int64_t wb = w8 ? 1 : 2;
   if (!aligned || a.K % kBK != 0) return false;
-  if ((a.N - 1) * a.ldw0 * 2 + a.K * 2 >= kLim) return false;
-  if (a.w1 && (a.N - 1) * a.ldw1 * 2 + a.K * 2 >= kLim) return false;
+  if (w8 && (!a.s0 || (a.w1 && !a.s1))) return false;
+  if ((a.N - 1) * a.ldw0 * wb + a.K * wb >= kLim) return false;
+  if (a.w1 && (a.N - 1) * a.ldw1 * wb + a.K * wb >= kLim) return false;
   if ((a.M - 1) * a.ldx * 2 + a.K * 2 >= kLim) return false;
   return true;
 }
@@ -490,26 +534,37 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup) {
   return best;
 }
 
-template <bool GATEUP>
+template <bool GATEUP, bool W8>
 int launch_gemm(const StreamArgs& a, hipStream_t s) {
   const GemmPlan p = gemm_plan_unsplit(a.M, a.N, a.K, GATEUP);
   switch (p.tile) {
-    case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3>(a, s);
-    case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(a, s);
-    case kT192x256: return launch_gemm_cfg<192, 256, 2, 4, GATEUP, 2>(a, s);
+    case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3, W8>(a, s);
+    case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, W8>(a, s);
+    case kT192x256: return launch_gemm_cfg<192, 256, 2, 4, GATEUP, 2, W8>(a, s);
     default: break;
   }
-  if (p.nmain == 0) return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(a, s);
+  if (p.nmain == 0) return launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2, W8>(a, s);
   StreamArgs m = a;
   m.N = p.nmain;
-  int e = launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2>(m, s);
+  int e = launch_gemm_cfg<256, 256, 4, 2, GATEUP, 2, W8>(m, s);
   if (e) return e;
+  // the tail: output columns nmain .. N-1 (weight rows and, for int8, their
+  // scales from nmain on)
   StreamArgs t = a;
   t.N = a.N - p.nmain;
-  t.w0 = static_cast<const uint16_t*>(a.w0) + p.nmain * a.ldw0;
-  if (GATEUP) t.w1 = static_cast<const uint16_t*>(a.w1) + p.nmain * a.ldw1;
+  if constexpr (W8) {
+    t.w0 = static_cast<const int8_t*>(a.w0) + p.nmain * a.ldw0;
+    t.s0 = a.s0 + p.nmain;
+    if (GATEUP) {
+      t.w1 = static_cast<const int8_t*>(a.w1) + p.nmain * a.ldw1;
+      t.s1 = a.s1 + p.nmain;
+    }
+  } else {
+    t.w0 = static_cast<const uint16_t*>(a.w0) + p.nmain * a.ldw0;
+    if (GATEUP) t.w1 = static_cast<const uint16_t*>(a.w1) + p.nmain * a.ldw1;
+  }
   t.y = a.y + p.nmain;
-  return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2>(t, s);
+  return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, W8>(t, s);
 }
 
 // When to split k across workgroups, measured on MI355X over Qwen3-0.6B/4B/8B
@@ -560,7 +615,7 @@ int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K
 }
 
 bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p) {
-  if (!a.ws || !gemm_supported(a, aligned)) return false;
+  if (!a.ws || !gemm_supported(a, aligned, false)) return false;
   *p = gemm_split_plan(a.M, a.N, a.K, gateup);
   return p->tile >= 0 && gemm_split_ws_floats(*p, a.M, a.N, a.K, gateup) <= a.ws_floats;
 }
@@ -578,8 +633,10 @@ int launch_gemm_split(const StreamArgs& a, const GemmSplit& p, hipStream_t s) {
 
 template int launch_gemm_split<false>(const StreamArgs&, const GemmSplit&, hipStream_t);
 template int launch_gemm_split<true>(const StreamArgs&, const GemmSplit&, hipStream_t);
-template int launch_gemm<false>(const StreamArgs&, hipStream_t);
-template int launch_gemm<true>(const StreamArgs&, hipStream_t);
+template int launch_gemm<false, false>(const StreamArgs&, hipStream_t);
+template int launch_gemm<true, false>(const StreamArgs&, hipStream_t);
+template int launch_gemm<false, true>(const StreamArgs&, hipStream_t);
+template int launch_gemm<true, true>(const StreamArgs&, hipStream_t);
 #endif
 
 }  // namespace fp

@@ -84,13 +84,27 @@ inline bool splitk8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (M < min_m || M > kSplitkMaxM8 || K % 64 != 0) return false;
   return M <= 64 || K <= 8192;
 }
+// Whether an int8 call of this shape runs gemm_kernel with in-register
+// dequantisation in preference to dequantising the weights into a workspace
+// first. Measured on MI355X (Qwen3-4B/8B): gate-up from 129 to 1024 rows (8B
+// at 256 rows: 121.7 -> 75.9 us), one weight stream of more than 4096 rows
+// with K <= 2560 from 129 to 512 rows (4B QKV at 256: 33.7 -> 28.4 us). With
+// more rows the dequantisation's VALU work costs 6-12% against the bf16 path
+// on dequantised weights; the long-K down projections keep that path with k
+// split across workgroups. Without a workspace every aligned int8 call of
+// more than 128 rows runs gemm_kernel.
+inline bool gemm8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
+  if (M <= kSplitkMaxM8 || K % 64 != 0) return false;
+  if (gateup) return M <= 1024;
+  return N > 4096 && K <= 2560 && M <= 512;
+}
 template <bool GATEUP, bool W8>
 int launch_splitk(const StreamArgs& a, hipStream_t s);
 
-// Direct-to-LDS bf16 MFMA contraction (fp_gemm.hip), used by launch_tiled
-// when gemm_supported() holds.
-bool gemm_supported(const StreamArgs& a, bool aligned);
-template <bool GATEUP>
+// Direct-to-LDS MFMA contraction (fp_gemm.hip; int8 weights dequantised in
+// registers), used by launch_tiled when gemm_supported() holds.
+bool gemm_supported(const StreamArgs& a, bool aligned, bool w8);
+template <bool GATEUP, bool W8>
 int launch_gemm(const StreamArgs& a, hipStream_t s);
 // The unsplit grid launch_gemm runs: tile (a GemmTile of fp_gemm.hip) and,
 // when nmain > 0, whole 256 x 256 rounds over the first nmain output columns

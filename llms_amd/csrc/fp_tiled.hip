@@ -212,9 +212,9 @@ int launch_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // to kSplitkMaxM rows against at most 8192 weight rows with K >=
 // kSplitkMinKTiled (Qwen3-4B QKV: 6144 x 2560), which give too few tiles for
 // 256 CUs and run the in-workgroup split-K tiles. int8 shapes that
-// splitk8_shape() admits run the split-K tiles too (in-register
-// dequantisation); other int8 calls, unaligned rows and K tails run
-// tiled_kernel.
+// splitk8_shape() admits run the split-K tiles too, other aligned int8 calls
+// with whole 64-wide k-steps run gemm_kernel (both dequantise in registers);
+// unaligned rows and K tails run tiled_kernel.
 template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
@@ -223,9 +223,12 @@ int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
   if (!W8 && a.M <= kSplitkMaxM && wrows <= kSplitkSmallN && a.K >= kSplitkMinKTiled &&
       splitk_supported(a, aligned, false))
     return launch_splitk<GATEUP, false>(a, s);
-  if (!W8 && gemm_supported(a, aligned)) return launch_gemm<GATEUP>(a, s);
+  if (!W8 && gemm_supported(a, aligned, false)) return launch_gemm<GATEUP, false>(a, s);
   if (W8 && splitk8_shape(a.M, a.N, a.K, GATEUP) && splitk_supported(a, aligned, true))
     return launch_splitk<GATEUP, true>(a, s);
+  // int8 that reaches here either suits the in-register gemm or had no
+  // workspace to dequantise into: gemm_kernel either way
+  if (W8 && gemm_supported(a, aligned, true)) return launch_gemm<GATEUP, true>(a, s);
   return launch_cfg<128, 128, 64, 2, 2, GATEUP, W8>(a, aligned, s);
 }
 

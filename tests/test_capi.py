@@ -281,3 +281,37 @@ def test_capi_raw_pointers_match_oracle():
     for yy in (y8, y9):
         p = ref.check_parity(bits(yy), out)
         assert p.ok, p
+
+
+@pytest.mark.gpu
+def test_int8_entry_points_without_workspace_prefill():
+    """The plain int8 entry points (no workspace to dequantise into) at
+    prefill sizes: gate-up, QKV and the long-K plain projection run the gemm
+    with in-register dequantisation."""
+    from llms_amd import _lib
+
+    lib = _lib.capi()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows = np.sort(np.random.default_rng(3).choice(2048, 64, replace=False))
+    for M, K, N, kind in [(2048, 2560, 1000, "gate-up"), (700, 2560, 4352, "qkv"), (512, 9728, 520, "linear")]:
+        x, w = qkv_inputs(700 + M, M, K, N, 0)
+        xd = x.cuda()
+        q = torch.empty(N, K, dtype=torch.int8, device="cuda")
+        s = torch.empty(N, dtype=torch.float32, device="cuda")
+        assert lib.fp_quantize_w8_per_row(_p(w.cuda()), K, _p(q), K, _p(s), N, K, stream) == 0
+        y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        r = rows[rows < M]
+        if kind == "gate-up":
+            st = lib.fp_gate_up_silu_w8(_p(xd), K, _p(q), K, _p(s), _p(q), K, _p(s), _p(y), N, M, N, K, stream)
+            out = lambda: ref.ref_gate_up_silu_w8_full(bits(x)[r], q.cpu().numpy(), s.cpu().numpy(),  # noqa: E731
+                                                       q.cpu().numpy(), s.cpu().numpy())
+        elif kind == "qkv":
+            st = lib.fp_qkv_w8(_p(xd), K, _p(q), K, _p(s), _p(y), N, M, N - 256, 128, K, stream)
+            out = lambda: ref.ref_qkv_w8_full(bits(x)[r], q.cpu().numpy(), s.cpu().numpy(), N - 256, 128)  # noqa: E731
+        else:
+            st = lib.fp_linear_w8(_p(xd), K, _p(q), K, _p(s), _p(y), N, M, N, K, stream)
+            out = lambda: ref.ref_linear_w8(bits(x)[r], q.cpu().numpy(), s.cpu().numpy())  # noqa: E731
+        assert st == 0, _lib.status_string(st)
+        torch.cuda.synchronize()
+        p = ref.check_parity(bits(y.cpu())[r], out())
+        assert p.ok, (kind, M, p)

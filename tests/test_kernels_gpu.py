@@ -448,6 +448,36 @@ def test_int8_split_k_tiles(M):
                f"int8 linear M={M} K={Kl} N={N}")
 
 
+@pytest.mark.parametrize("M", [129, 300, 1024])
+def test_int8_gemm_in_register(M):
+    """The prefill gemm with int8 weight tiles dequantised in registers:
+    gate-up with a partial last tile and an all-zero weight row, QKV with more
+    than 4096 outputs, and the dequantisation bit for bit (one-hot x rows give
+    single dequantised weights)."""
+    kern = _kernels()
+    K = 2560
+    x, wg, wu = ffn_inputs(600 + M, M, K, 1000)
+    wg[11] = 0
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+    rows = _rows(M, limit=96)
+    _check(y[rows], ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                                 qu.cpu().numpy(), su.cpu().numpy()),
+           f"int8 gemm gate-up M={M} N=1000")
+    if M > 512:
+        return
+    n_q, n_k = 4096, 128
+    _, w = qkv_inputs(610 + M, 1, K, n_q, n_k, w_std=0.05)
+    q, s = _quant(w)
+    deq = ref.dequant_w8(q.cpu().numpy(), s.cpu().numpy())
+    ks = np.random.default_rng(M).choice(K, size=M, replace=False)
+    xo = torch.zeros(M, K, dtype=torch.bfloat16)
+    xo[np.arange(M), ks] = 1.0
+    yq, yk, yv = kern.fused_qkv_w8(xo.to(DEV), q, s, n_q=n_q, n_k=n_k)
+    np.testing.assert_array_equal(bits(torch.cat([yq, yk, yv], -1).cpu()), deq[:, ks].T)
+
+
 def test_int8_tails_and_zero_rows():
     kern = _kernels()
     for M, K, N in [(3, 2541, 100), (70, 2541, 100), (5, 1040, 48), (90, 1040, 48),
@@ -560,13 +590,18 @@ def test_split_k_across_workgroups(M, N, K, op):
                                          (128, 9728, 2560, "linear", True),
                                          (128, 4096, 2560, "linear", False),
                                          (512, 9728, 2560, "linear", True),
-                                         (300, 2560, 9728, "gate-up", True)])
+                                         (300, 2560, 9728, "gate-up", False),
+                                         (1100, 2560, 1000, "gate-up", True),
+                                         (200, 2560, 4352, "qkv", False),
+                                         (600, 2560, 4352, "qkv", True)])
 def test_int8_dequantised_mfma_path(M, K, N, op, dq):
     """With enough rows the int8 calls dequantise the weights into the
     workspace and run the bf16 path (split across workgroups where planned);
-    the contract is unchanged. Below the threshold, and where the int8 split-K
-    tiles take the shape (K % 64 == 0, up to 128 rows, K <= 8192 above 64),
-    the in-register int8 kernels run."""
+    the contract is unchanged. Below the threshold, where the int8 split-K
+    tiles take the shape (K % 64 == 0, up to 128 rows, K <= 8192 above 64) and
+    where the int8 gemm does (gate-up up to 1024 rows, one weight stream of
+    more than 4096 rows with K <= 2560 up to 512 rows), the in-register int8
+    kernels run."""
     from llms_amd import _lib
 
     gu = op == "gate-up"
