@@ -27,14 +27,17 @@ namespace fp {
 
 namespace {
 
-constexpr int kBK = 64;          // k per LDS stage
-constexpr int kCPR = kBK / 8;    // 16-byte chunks per tile row
-constexpr int kRPI = 1024 / (kBK * 2);  // tile rows per load instruction
+constexpr int kBK = 64;          // k per LDS stage (bf16 unsplit tiles may take 128)
 constexpr int kGroupM = 8;       // m-tiles per group of the tile order
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-__device__ __forceinline__ int swz(int r) { return (r >> 1) & (kCPR - 1); }
+// XOR swizzle of the 16-byte chunks of bf16 tile row r at a k-step of BK:
+// 64 (8 chunks per row, chunk c stored at c ^ ((r >> 1) & 7)) or 128 (16
+// chunks, at c ^ (r & 15)); either way the 16 rows that one fragment read
+// touches land on distinct LDS banks.
+template <int BK>
+__device__ __forceinline__ int swzk(int r) { return BK == 64 ? (r >> 1) & 7 : r & 15; }
 __device__ __forceinline__ int swz8(int r) { return (r >> 2) & 3; }
 
 // buffer_load_dwordx4 ... lds: 16 bytes per lane from base + voff + soff into
@@ -60,20 +63,24 @@ constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >>
 // c ^ ((r >> 2) & 3)); each lane turns the 8 int8 of its MFMA A fragment into
 // bf16(q * s) in registers (dequant8_bf16: the dequantise-then-matmul
 // rounding) before the bf16 MFMA.
-template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool SPLIT = false, bool W8 = false>
+template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool SPLIT = false, bool W8 = false,
+          int BK = kBK>
 __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int n_mt, int n_nt,
                                                               int ksteps, float* ws) {
   constexpr int NW = WN * WM;
+  constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
+  constexpr int RPI = 1024 / (BK * 2);        // tile rows per load instruction
+  static_assert(BK == kBK || (BK == 2 * kBK && !W8 && !SPLIT), "k-step: 64, or 128 for bf16 unsplit");
   constexpr int TN = BN / WN, TM = BM / WM;   // per-wave tile
   constexpr int FN = TN / 16, FM = TM / 16;   // MFMA sub-tiles per wave
   constexpr int WB = W8 ? 1 : 2;              // bytes per weight element
-  constexpr int WKE = kBK * WB / 2;           // weight LDS row, in 16-bit units
-  constexpr int WRPI = W8 ? 16 : kRPI;        // weight rows per load instruction
-  constexpr int WCPR = W8 ? 4 : kCPR;         // 16-byte chunks per weight row
+  constexpr int WKE = BK * WB / 2;           // weight LDS row, in 16-bit units
+  constexpr int WRPI = W8 ? 16 : RPI;        // weight rows per load instruction
+  constexpr int WCPR = W8 ? 4 : CPR;         // 16-byte chunks per weight row
   constexpr int NWI = BN / WRPI;              // weight load instructions per stage
   constexpr int IW = (NWI + NW - 1) / NW;     // ... per wave (the last may be idle)
-  constexpr int IX = BM / kRPI / NW;          // x load instructions per wave per stage
-  static_assert(BN % WRPI == 0 && BM % (kRPI * NW) == 0, "tile/waves");
+  constexpr int IX = BM / RPI / NW;          // x load instructions per wave per stage
+  static_assert(BN % WRPI == 0 && BM % (RPI * NW) == 0, "tile/waves");
   static_assert(W8 || NWI % NW == 0, "bf16 weight loads spread evenly over the waves");
   // with three stages the waits count a wave's loads per step, so they must
   // be the same for every wave
@@ -88,9 +95,9 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   __shared__ __attribute__((aligned(1024))) uint16_t sW0[BN][WKE];
   __shared__ __attribute__((aligned(1024))) uint16_t sW1[BN][WKE];
   __shared__ __attribute__((aligned(1024))) uint16_t sW2[NS > 2 ? BN : 1][WKE];
-  __shared__ __attribute__((aligned(1024))) uint16_t sX0[BM][kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sX1[BM][kBK];
-  __shared__ __attribute__((aligned(1024))) uint16_t sX2[NS > 2 ? BM : 1][kBK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sX0[BM][BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sX1[BM][BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sX2[NS > 2 ? BM : 1][BK];
 
   const int lane = threadIdx.x & (kWave - 1);
   // wave index as a scalar: load instructions, LDS bases and buffer
@@ -116,14 +123,15 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   const int64_t m0 = (int64_t)tm * BM;
   const int64_t c0 = (int64_t)tn * (GATEUP ? BN / 2 : BN);  // first output column
 
-  // Load instruction q (q = wave + NW*j) fills tile rows 8q..8q+7 with
+  // Load instruction q (q = wave + NW*j) fills tile rows RPI q .. RPI q + RPI-1
+  // (RPI = 8 at a k-step of 64, 4 at 128; int8 weights: 16) with
   // buffer_load_dwordx4 ... lds: the matrix base lives in a buffer resource
   // (SGPRs), the k-step in soffset, and each lane carries one 32-bit byte
   // offset (row * stride + chunk). The resource size is the matrix size, so
   // rows past the end read as zeros. The dispatcher guarantees matrix byte
   // sizes below 2^32.
-  const int lrow = lane / kCPR;                 // row within an instruction's 8
-  const int lchunk = lane % kCPR;               // LDS chunk position it fills
+  const int lrow = lane / CPR;                 // row within an instruction's RPI
+  const int lchunk = lane % CPR;               // LDS chunk position it fills
   // weight tile row t: output n(t) of matrix Wu when up(t) (gate-up tiles
   // interleave 16-row groups of Wg and Wu)
   auto wrow_n = [&](int t) -> int64_t { return GATEUP ? c0 + (t / 32) * 16 + (t % 16) : c0 + t; };
@@ -135,13 +143,13 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
     const int t = q * WRPI + lane / WCPR;
     const int c = lane % WCPR;
     const int64_t ld = wrow_up(t) ? a.ldw1 : a.ldw0;
-    woff[j] = (uint32_t)(wrow_n(t) * ld * WB) + (uint32_t)((c ^ (W8 ? swz8(t) : swz(t))) * 16);
+    woff[j] = (uint32_t)(wrow_n(t) * ld * WB) + (uint32_t)((c ^ (W8 ? swz8(t) : swzk<BK>(t))) * 16);
   }
   uint32_t xoff[IX];
 #pragma unroll
   for (int j = 0; j < IX; ++j) {
-    const int t = (wave + NW * j) * kRPI + lrow;
-    xoff[j] = (uint32_t)((m0 + t) * a.ldx * 2) + (uint32_t)((lchunk ^ swz(t)) * 16);
+    const int t = (wave + NW * j) * RPI + lrow;
+    xoff[j] = (uint32_t)((m0 + t) * a.ldx * 2) + (uint32_t)((lchunk ^ swzk<BK>(t)) * 16);
   }
   // byte sizes of the buffer resources (rows past them read as zeros)
   const int wbytes0 = (int)((a.N - 1) * a.ldw0 * WB + a.K * WB);
@@ -161,7 +169,7 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
     }
   }
 
-  auto issue = [&](uint16_t (*tw)[WKE], uint16_t (*tx)[kBK], int64_t k0) {
+  auto issue = [&](uint16_t (*tw)[WKE], uint16_t (*tx)[BK], int64_t k0) {
     const uint32_t kb = (uint32_t)(k0 * 2);
 #pragma unroll
     for (int j = 0; j < IW; ++j) {
@@ -174,7 +182,7 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
     }
 #pragma unroll
     for (int j = 0; j < IX; ++j)
-      load_lds16(a.x, xbytes, (lds_ptr_t)&tx[(wave + NW * j) * kRPI][0], xoff[j], kb);
+      load_lds16(a.x, xbytes, (lds_ptr_t)&tx[(wave + NW * j) * RPI][0], xoff[j], kb);
   };
 
   f32x4 acc[FN][FM];
@@ -184,34 +192,34 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Fragment addresses: sub-tile i of a wave reads tile row base + 16 i + li,
-  // and swz() of that row does not depend on i (16 i only touches row bits
+  // and swzk<BK>() of that row does not depend on i (16 i only touches row bits
   // above the swizzle), so every fragment address is one per-lane byte offset
-  // plus the compile-time constants 16 i * 128 and the stage base. k-substep
-  // kk = 1 flips chunk bit 2 (chunk (4 + grp) ^ s = (grp ^ s) ^ 4).
+  // plus the compile-time constants 16 i * 2 BK and the stage base. k-substep
+  // kk flips chunk bits 2.. (chunk (4 kk + grp) ^ s = (grp ^ s) ^ 4 kk).
   const int ra = wn * TN + li, rb = wm * TM + li;
   // int8: 8 bytes at chunk 2 kk + (grp >> 1), half grp & 1 (k-substep kk
   // flips chunk bit 1)
   const uint32_t offa =
-      W8 ? (uint32_t)(ra * kBK + ((((grp >> 1) ^ swz8(ra)) * 16) | ((grp & 1) * 8)))
-         : (uint32_t)(ra * kBK * 2 + ((grp ^ swz(ra)) * 16));
-  const uint32_t offb = (uint32_t)(rb * kBK * 2 + ((grp ^ swz(rb)) * 16));
-  auto compute = [&](const uint16_t (*tw)[WKE], const uint16_t (*tx)[kBK]) {
+      W8 ? (uint32_t)(ra * BK + ((((grp >> 1) ^ swz8(ra)) * 16) | ((grp & 1) * 8)))
+         : (uint32_t)(ra * BK * 2 + ((grp ^ swzk<BK>(ra)) * 16));
+  const uint32_t offb = (uint32_t)(rb * BK * 2 + ((grp ^ swzk<BK>(rb)) * 16));
+  auto compute = [&](const uint16_t (*tw)[WKE], const uint16_t (*tx)[BK]) {
 #pragma unroll
-    for (int kk = 0; kk < kBK / 32; ++kk) {
+    for (int kk = 0; kk < BK / 32; ++kk) {
       const uint32_t oa = offa ^ (uint32_t)(kk * (W8 ? 32 : 64)), ob = offb ^ (uint32_t)(kk * 64);
       u32x4 fa[FN], fb[FM];
 #pragma unroll
       for (int i = 0; i < FN; ++i) {
         if constexpr (W8) {
-          const u32x2 q = *reinterpret_cast<const u32x2*>((const char*)tw + oa + i * 16 * kBK);
+          const u32x2 q = *reinterpret_cast<const u32x2*>((const char*)tw + oa + i * 16 * BK);
           fa[i] = dequant8_bf16(q.x, q.y, sc[i], nsc[i]);
         } else {
-          fa[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * kBK * 2);
+          fa[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * BK * 2);
         }
       }
 #pragma unroll
       for (int j = 0; j < FM; ++j)
-        fb[j] = *reinterpret_cast<const u32x4*>((const char*)tx + ob + j * 16 * kBK * 2);
+        fb[j] = *reinterpret_cast<const u32x4*>((const char*)tx + ob + j * 16 * BK * 2);
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -222,7 +230,7 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
     }
   };
   auto stw = [&](int s) -> uint16_t (*)[WKE] { return s == 0 ? sW0 : (s == 1 ? sW1 : sW2); };
-  auto stx = [&](int s) -> uint16_t (*)[kBK] { return s == 0 ? sX0 : (s == 1 ? sX1 : sX2); };
+  auto stx = [&](int s) -> uint16_t (*)[BK] { return s == 0 ? sX0 : (s == 1 ? sX1 : sX2); };
 
   // Ring of NS stages: k-step k lives in stage k % NS, and while step k is
   // consumed steps k+1 .. k+NS-1 are in flight. After a step, wait until this
@@ -230,12 +238,12 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   // flight), then for every wave's.
   constexpr int kPerStep = IW + IX;  // load instructions per wave per step (even loads)
   const int64_t kfirst = (int64_t)ks * ksteps;  // first k-step of this workgroup
-  const int64_t nleft = a.K / kBK - kfirst;
-  const int64_t nkt = SPLIT ? (ksteps < nleft ? (int64_t)ksteps : nleft) : a.K / kBK;
-  const int64_t kb0 = kfirst * kBK;
+  const int64_t nleft = a.K / BK - kfirst;
+  const int64_t nkt = SPLIT ? (ksteps < nleft ? (int64_t)ksteps : nleft) : a.K / BK;
+  const int64_t kb0 = kfirst * BK;
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nkt) issue(stw(s), stx(s), kb0 + s * kBK);
+    if (s < nkt) issue(stw(s), stx(s), kb0 + s * BK);
   if (nkt > NS - 2)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * kPerStep));
   else
@@ -247,7 +255,7 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
       const int64_t k = kt + u;
       if (k >= nkt) break;
       const bool steady = k + NS - 1 < nkt;
-      if (steady) issue(stw((u + NS - 1) % NS), stx((u + NS - 1) % NS), kb0 + (k + NS - 1) * kBK);
+      if (steady) issue(stw((u + NS - 1) % NS), stx((u + NS - 1) % NS), kb0 + (k + NS - 1) * BK);
       compute(stw(u), stx(u));
       if (steady)
         __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * kPerStep));
@@ -372,12 +380,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int
 
 }  // namespace
 
-template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool W8 = false>
+template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool W8 = false, int BK = kBK>
 int launch_gemm_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t cols = GATEUP ? BN / 2 : BN;
   const int n_nt = (int)((a.N + cols - 1) / cols);
   const int n_mt = (int)((a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm_kernel<BN, BM, WN, WM, GATEUP, NS, false, W8>), dim3((unsigned)(n_nt * n_mt)),
+  hipLaunchKernelGGL((gemm_kernel<BN, BM, WN, WM, GATEUP, NS, false, W8, BK>), dim3((unsigned)(n_nt * n_mt)),
                      dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt, 0, (float*)nullptr);
   return (int)hipGetLastError();
 }
@@ -433,12 +441,16 @@ bool gemm_supported(const StreamArgs& a, bool aligned, bool w8) {
 }
 
 // Tiles the dispatcher uses: {weight rows, x rows, workgroups per CU (LDS)}.
-enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256, kT192x256 };
+// kK*: bf16 tiles with 128-wide k-steps (two LDS stages: 64 KB, 112 KB and
+// 128 KB).
+enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256, kT192x256,
+                kK64x64, kK96x128, kK128x128 };
 struct TileInfo {
   int bn, bm, per_cu;
 };
 constexpr TileInfo kTiles[] = {{64, 32, 4},   {128, 64, 3},  {64, 128, 2},
-                               {128, 128, 2}, {256, 256, 1}, {192, 256, 1}};
+                               {128, 128, 2}, {256, 256, 1}, {192, 256, 1},
+                               {64, 64, 2},   {96, 128, 1},  {128, 128, 1}};
 constexpr int kCUs = 256;
 
 int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
@@ -499,7 +511,9 @@ double grid_cost(int tile, int64_t M, int64_t N, int64_t nkt, bool gateup) {
          (double)(pairs + singles) * c.tile;
 }
 
-// The unsplit plan: the cheapest of 64 x 128, 128 x 128, 256 x 256, 192 x 256, and
+// The unsplit plan: for bf16 weights a single round of k-step-128 tiles where
+// one fits (k128_tile); otherwise the cheapest of 64 x 128, 128 x 128,
+// 256 x 256, 192 x 256, and
 // "256 x 256 for whole rounds + a 128 x 128 tail" (nmain > 0: the first
 // nmain output columns as whole 256 x 256 rounds, the rest as 128 x 128 tiles
 // in a second launch). The tail form turns the last partial round of 256 x
@@ -510,7 +524,62 @@ double grid_cost(int tile, int64_t M, int64_t N, int64_t nkt, bool gateup) {
 // the model: where 128 x 128 tiles would run one per CU and 64 x 128 tiles at
 // most two, 64 x 128 is faster on every shape measured (the pair of smaller
 // tiles hides latency better than one tile of the same work).
-GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup) {
+// Grids of tiles with 128-wide k-steps: twice the bytes per load round and
+// half the per-step waits and barriers of the 64-wide tiles. Measured on
+// MI355X (Qwen3-0.6B/4B/8B QKV, o, down and gate-up, M = 160..2048; results
+// bit-identical to the 64-wide plans), they win wherever the whole grid runs
+// in one round (at most one tile per CU, two for 64 x 64): 4B QKV M = 512
+// 37.6 -> 30.2 us (96 x 128), 0.6B QKV M = 512 13.7 -> 9.9 us (64 x 64), 8B
+// QKV M = 512 59.5 -> 44.3 us, 4B o M = 1536 48.8 -> 37.6 us; with more
+// rounds they lose to the plans above (up to 50% slower). Gate-up only with
+// weights under 2^24 elements (0.6B M = 160..640: 13.3 -> 9.5 us; 4B/8B
+// gate-up tiles of 128 x 128 run 11-22% slower with 128-wide steps than
+// with 64-wide ones). 96 x 128 (QKV-like outputs only: its gate/up pairing
+// would need one wave column) where 96 divides N, in place of 128 x 128
+// (4-10% faster there; with a partial last tile 5-22% slower). Between 64 x
+// 64 and the larger tile, the cost fixed + k-steps x per-step decides,
+// where a tile alone on its CU costs more per step the more CUs are busy
+// (relative units, fitted to the same measurements).
+struct K128Cost {
+  double fixed, one, busy, pair;
+};
+constexpr K128Cost kCostK64x64{0.0, 0.664, 0.199, 0.912};
+constexpr K128Cost kCostK96x128{2.065, 1.082, 0.203, 0.0};
+constexpr K128Cost kCostK128x128{0.175, 1.134, 0.294, 0.0};
+
+// The k-step-128 tile of a single-round grid for this call, -1 if none.
+int k128_tile(int64_t M, int64_t N, int64_t K, bool gateup) {
+  if (K % (2 * kBK) != 0) return -1;
+  if (gateup && 2 * N * K >= ((int64_t)1 << 24)) return -1;
+  const int64_t nkt = K / (2 * kBK);
+  const bool use96 = !gateup && N % 96 == 0 && tile_count(kK96x128, M, N, false) <= kCUs;
+  int best = -1;
+  double cbest = 0.0;
+  for (int t : {kK64x64, use96 ? kK96x128 : kK128x128}) {
+    const int64_t n = tile_count(t, M, N, gateup);
+    if (n > kCUs * kTiles[t].per_cu) continue;
+    const K128Cost& c = t == kK64x64 ? kCostK64x64 : t == kK96x128 ? kCostK96x128 : kCostK128x128;
+    const double busy = (double)(n < kCUs ? n : kCUs) / kCUs;
+    const double step = n > kCUs ? c.pair : c.one + c.busy * busy;
+    const double cost = c.fixed + (double)nkt * step;
+    if (best < 0 || cost < cbest) best = t, cbest = cost;
+  }
+  return best;
+}
+
+// Whether a single round of k-step-128 tiles (k128_tile) has at least one
+// tile per 20 columns of K: enough tiles against the k loop that splitting k
+// (across or inside workgroups) no longer pays.
+bool k128_wide(int64_t M, int64_t N, int64_t K, bool gateup) {
+  const int t = k128_tile(M, N, K, gateup);
+  return t >= 0 && tile_count(t, M, N, gateup) * 20 >= K;
+}
+
+GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf16) {
+  if (bf16) {
+    const int t = k128_tile(M, N, K, gateup);
+    if (t >= 0) return GemmPlan{t, 0};
+  }
   const int64_t nkt = K / kBK;
   GemmPlan best{kT64x128, 0};
   double cbest = grid_cost(kT64x128, M, N, nkt, gateup);
@@ -536,7 +605,17 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup) {
 
 template <bool GATEUP, bool W8>
 int launch_gemm(const StreamArgs& a, hipStream_t s) {
-  const GemmPlan p = gemm_plan_unsplit(a.M, a.N, a.K, GATEUP);
+  const GemmPlan p = gemm_plan_unsplit(a.M, a.N, a.K, GATEUP, !W8);
+  if constexpr (!W8) {
+    switch (p.tile) {
+      case kK64x64: return launch_gemm_cfg<64, 64, 2, 2, GATEUP, 2, false, 128>(a, s);
+      case kK128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, false, 128>(a, s);
+      case kK96x128:
+        if constexpr (!GATEUP) return launch_gemm_cfg<96, 128, 2, 2, false, 2, false, 128>(a, s);
+        return (int)hipErrorInvalidValue;  // never planned for gate-up
+      default: break;
+    }
+  }
   switch (p.tile) {
     case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3, W8>(a, s);
     case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, W8>(a, s);
@@ -581,7 +660,14 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
 // Tile by rows: 64 x 32 to 32 rows, 128 x 64 to 128, 128 x 128 (64 x 128
 // for outputs of at most 1024 columns) to 1024 rows or narrow outputs,
 // 256 x 256 above; splits = slots / tiles rounded, in 2..16 with at least
-// 8 k-steps each.
+// 8 k-steps each. No split where a single round of k-step-128 tiles can run
+// instead (k128_tile) with K <= 4096 and either at most 3 splits, or at most
+// 6 with weights under 2^24 elements and one tile per 20 columns of K
+// (k128_wide) (measured: 4B QKV M = 256 28.6 -> 18.5 us, 4B o M = 640
+// 35.1 -> 26.6 us, 8B o M = 1024 49.4 -> 47.8 us, 0.6B o M = 1024 20.9 ->
+// 14.3 us; with 8 splits, 4-5 over 8B QKV and o weights, or rounds of few
+// tiles against K, such as 0.6B o and down below 256 rows, the split is
+// 5-36% faster).
 GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
   const GemmSplit none{-1, 1};
   if (M < 32 || K % kBK != 0) return none;
@@ -606,7 +692,11 @@ GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
   ns = ns < 16 ? ns : 16;
   ns = ns < nkt / 8 ? ns : nkt / 8;
   if (ns < 2) return none;
-  return GemmSplit{tile, gemm_splitk_used(K, (int)ns)};
+  const int used = gemm_splitk_used(K, (int)ns);
+  if (K <= 4096 && k128_tile(M, N, K, gateup) >= 0 &&
+      (used <= 3 || (used <= 6 && wrows * K < ((int64_t)1 << 24) && k128_wide(M, N, K, gateup))))
+    return none;
+  return GemmSplit{tile, used};
 }
 
 int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K, bool gateup) {

@@ -108,12 +108,16 @@ template <bool GATEUP, bool W8>
 int launch_gemm(const StreamArgs& a, hipStream_t s);
 // The unsplit grid launch_gemm runs: tile (a GemmTile of fp_gemm.hip) and,
 // when nmain > 0, whole 256 x 256 rounds over the first nmain output columns
-// followed by 128 x 128 tiles over the rest.
+// followed by 128 x 128 tiles over the rest. bf16: whether the tiles with
+// 128-wide k-steps (bf16 weights only) are candidates.
 struct GemmPlan {
   int tile;
   int64_t nmain;
 };
-GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup);
+GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf16);
+// Whether the bf16 plan is a single round of tiles with 128-wide k-steps with
+// at least one tile per 20 columns of K (then it beats the split-K tiles).
+bool k128_wide(int64_t M, int64_t N, int64_t K, bool gateup);
 // k split across workgroups — for calls whose tile grid leaves the chip
 // partly idle while each tile has a long k loop — with fp32 partials in the
 // caller's workspace and a fixed-order reduce (fp_gemm.hip). tile < 0: no

@@ -210,8 +210,11 @@ int launch_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // loads, XCD-aware order): split across workgroups when the plan says so and
 // the caller gave a workspace, else unsplit — except, without the split, up
 // to kSplitkMaxM rows against at most 8192 weight rows with K >=
-// kSplitkMinKTiled (Qwen3-4B QKV: 6144 x 2560), which give too few tiles for
-// 256 CUs and run the in-workgroup split-K tiles. int8 shapes that
+// kSplitkMinKTiled, which give too few tiles for 256 CUs and run the
+// in-workgroup split-K tiles, unless a round of tiles with 128-wide k-steps
+// has one tile per 20 columns of K (k128_wide: Qwen3-4B QKV, 6144 x 2560, at
+// 65-256 rows: 17.6-33.3 -> 16.9-18.5 us; 8B QKV below 160 rows, 4B o and
+// 0.6B o and down keep the split-K tiles, 5-20% faster there). int8 shapes that
 // splitk8_shape() admits run the split-K tiles too, other aligned int8 calls
 // with whole 64-wide k-steps run gemm_kernel (both dequantise in registers);
 // unaligned rows and K tails run tiled_kernel.
@@ -221,7 +224,7 @@ int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
   GemmSplit sp;
   if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP>(a, sp, s);
   if (!W8 && a.M <= kSplitkMaxM && wrows <= kSplitkSmallN && a.K >= kSplitkMinKTiled &&
-      splitk_supported(a, aligned, false))
+      splitk_supported(a, aligned, false) && !k128_wide(a.M, a.N, a.K, GATEUP))
     return launch_splitk<GATEUP, false>(a, s);
   if (!W8 && gemm_supported(a, aligned, false)) return launch_gemm<GATEUP, false>(a, s);
   if (W8 && splitk8_shape(a.M, a.N, a.K, GATEUP) && splitk_supported(a, aligned, true))

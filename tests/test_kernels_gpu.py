@@ -284,24 +284,31 @@ def test_qwen3_4b_prefill_8192_rows():
     check_ffn(8192, 8192, K, I, label="4B gate-up M=8192 (row subset)")
 
 
-# Row counts whose prefill grids differ on Qwen3-4B shapes: 64 x 128 (gate-up
-# 128 rows, QKV 384), 128 x 128 (gate-up 384, QKV 768), 192 x 256 (gate-up 512,
-# QKV 1536 and 2048) and 256 x 256 tiles (gate-up 1536), and whole 256 x 256
-# rounds followed by a 128 x 128 tail launch (gate-up 1024 and 2048, QKV 3072).
-PLAN_ROWS = {"gate_up": (2048, [128, 384, 512, 1024, 1536]),
-             "qkv": (3072, [384, 768, 1536, 2048])}
+# Row counts whose prefill grids differ. Qwen3-4B: 64 x 64 tiles with
+# 128-wide k-steps (QKV 96 and 256 rows), 96 x 128 (QKV 384) and 128 x 128
+# (QKV 640) with 128-wide k-steps, 64 x 128 (gate-up 128 rows), 128 x 128
+# (gate-up 384, QKV 768), 192 x 256 (gate-up 512, QKV 1536 and 2048) and
+# 256 x 256 tiles (gate-up 1536), and whole 256 x 256 rounds followed by a
+# 128 x 128 tail launch (gate-up 1024 and 2048, QKV 3072). Qwen3-0.6B: 64 x 64
+# (gate-up 96 and 320, QKV 128) and 128 x 128 (gate-up 512, QKV 640) with
+# 128-wide k-steps, 128 x 128 (gate-up 1024, QKV 1536 and 3072) and 192 x 256
+# (gate-up 2048).
+PLAN_ROWS = {"gate_up": (QWEN3_4B, 2048, [128, 384, 512, 1024, 1536]),
+             "qkv": (QWEN3_4B, 3072, [96, 256, 384, 640, 768, 1536, 2048]),
+             "gate_up_0.6b": (QWEN3_0_6B, 2048, [96, 320, 512, 1024]),
+             "qkv_0.6b": (QWEN3_0_6B, 3072, [128, 640, 1536])}
 
 
 @pytest.mark.parametrize("kind", list(PLAN_ROWS))
 def test_prefill_rows_independent_of_grid_plan(kind):
-    """Every prefill grid plan contracts each output over the same k-steps in
-    the same order, so a row's bits do not depend on how many rows the call
-    has (and with it which tiles, or which of two launches, computed it). The
-    largest call is checked against the oracle on a row subset; the smaller
-    calls must reproduce its rows bit for bit."""
-    K, n_q, n_k, I = QWEN3_4B
-    M_full, Ms = PLAN_ROWS[kind]
-    if kind == "qkv":
+    """Every unsplit prefill grid plan (64- or 128-wide k-steps, one launch or
+    two) contracts each output over k in the same order, so a row's bits do
+    not depend on how many rows the call has (and with it which tiles, or
+    which of two launches, computed it). The largest call is checked against
+    the oracle on a row subset; the smaller calls must reproduce its rows bit
+    for bit."""
+    (K, n_q, n_k, I), M_full, Ms = PLAN_ROWS[kind]
+    if kind.startswith("qkv"):
         x, w = qkv_inputs(77, M_full, K, n_q, n_k)
         xd, wd = x.to(DEV), w.to(DEV)
 
@@ -310,7 +317,7 @@ def test_prefill_rows_independent_of_grid_plan(kind):
             return torch.cat([q, k, v], dim=-1).cpu()
         y = run(xd)
         rows = _rows(M_full)
-        _check(y[rows], ref.ref_qkv_full(bits(x)[rows], bits(w), n_q, n_k), f"qkv M={M_full}")
+        _check(y[rows], ref.ref_qkv_full(bits(x)[rows], bits(w), n_q, n_k), f"{kind} M={M_full}")
     else:
         x, wg, wu = ffn_inputs(77, M_full, K, I)
         xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
@@ -320,7 +327,7 @@ def test_prefill_rows_independent_of_grid_plan(kind):
         y = run(xd)
         rows = _rows(M_full)
         _check(y[rows], ref.ref_gate_up_silu_full(bits(x)[rows], bits(wg), bits(wu)),
-               f"gate-up M={M_full}")
+               f"{kind} M={M_full}")
     for M in Ms:
         ym = run(xd[:M].contiguous())
         assert torch.equal(ym.view(torch.int16), y[:M].view(torch.int16)), f"{kind} M={M}"
@@ -551,7 +558,7 @@ def test_linear_tails(M, K, N):
 
 @pytest.mark.parametrize("M,N,K,op", [
     (32, 2560, 9728, "linear"), (100, 4096, 12288, "linear"), (300, 1001, 8192, "linear"),
-    (1024, 2560, 9728, "linear"), (2048, 1024, 3072, "linear"), (256, 6144, 2560, "qkv"),
+    (1024, 2560, 9728, "linear"), (2048, 2560, 9728, "linear"), (256, 6144, 4096, "qkv"),
     (64, 12288, 4096, "gate-up"), (200, 1001, 8192, "gate-up"), (77, 4096, 4096, "linear")])
 def test_split_k_across_workgroups(M, N, K, op):
     """Calls the planner splits across workgroups (fp32 partials in a torch
