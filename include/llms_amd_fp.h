@@ -173,9 +173,12 @@ int fp_linear_bf16_ws(const void* x, int64_t ldx,
  * given that much
  * workspace, the int8 weights are dequantised once into the workspace as
  * bf16(q * s) — the exact weight the int8 contract computes with — and the
- * bf16 MFMA path (k split across workgroups included) runs on them; results
- * stay within the same contract. Without a workspace, or with fewer rows, the
- * in-register dequantising kernels of the plain entry points run.
+ * bf16 MFMA path runs on them; where that path would split k across at least
+ * 4 workgroups, the split runs on the int8 weights directly (dequantised in
+ * registers, bit-identical result) and the workspace holds only its fp32
+ * partials. Results stay within the same contract. Without a workspace, or
+ * with fewer rows, the in-register dequantising kernels of the plain entry
+ * points run.
  */
 int64_t fp_workspace_bytes_w8(int64_t M, int64_t N, int64_t K, int gate_up);
 

@@ -407,14 +407,14 @@ int64_t gemm_splitk_ws_floats(const StreamArgs& a, int nsplit) {
   return (int64_t)gemm_splitk_used(a.K, nsplit) * a.M * (GATEUP ? 2 * a.N : a.N);
 }
 
-template <int BN, int BM, int WN, int WM, bool GATEUP, int NS>
+template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool W8 = false>
 int launch_gemm_splitk_cfg(const StreamArgs& a, int nsplit, float* ws, hipStream_t s) {
   const int64_t cols = GATEUP ? BN / 2 : BN;
   const int n_nt = (int)((a.N + cols - 1) / cols);
   const int n_mt = (int)((a.M + BM - 1) / BM);
   const int per = (int)gemm_splitk_ksteps(a.K, nsplit);
   const int used = gemm_splitk_used(a.K, nsplit);
-  hipLaunchKernelGGL((gemm_kernel<BN, BM, WN, WM, GATEUP, NS, true>),
+  hipLaunchKernelGGL((gemm_kernel<BN, BM, WN, WM, GATEUP, NS, true, W8>),
                      dim3((unsigned)(n_nt * n_mt * used)), dim3(WN * WM * kWave), 0, s, a, n_mt,
                      n_nt, per, ws);
   int e = (int)hipGetLastError();
@@ -710,19 +710,21 @@ bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p
   return p->tile >= 0 && gemm_split_ws_floats(*p, a.M, a.N, a.K, gateup) <= a.ws_floats;
 }
 
-template <bool GATEUP>
+template <bool GATEUP, bool W8>
 int launch_gemm_split(const StreamArgs& a, const GemmSplit& p, hipStream_t s) {
   switch (p.tile) {
-    case kT64x32: return launch_gemm_splitk_cfg<64, 32, 2, 2, GATEUP, 3>(a, p.nsplit, a.ws, s);
-    case kT128x64: return launch_gemm_splitk_cfg<128, 64, 4, 2, GATEUP, 2>(a, p.nsplit, a.ws, s);
-    case kT64x128: return launch_gemm_splitk_cfg<64, 128, 2, 2, GATEUP, 3>(a, p.nsplit, a.ws, s);
-    case kT128x128: return launch_gemm_splitk_cfg<128, 128, 4, 2, GATEUP, 2>(a, p.nsplit, a.ws, s);
-    default: return launch_gemm_splitk_cfg<256, 256, 4, 2, GATEUP, 2>(a, p.nsplit, a.ws, s);
+    case kT64x32: return launch_gemm_splitk_cfg<64, 32, 2, 2, GATEUP, 3, W8>(a, p.nsplit, a.ws, s);
+    case kT128x64: return launch_gemm_splitk_cfg<128, 64, 4, 2, GATEUP, 2, W8>(a, p.nsplit, a.ws, s);
+    case kT64x128: return launch_gemm_splitk_cfg<64, 128, 2, 2, GATEUP, 3, W8>(a, p.nsplit, a.ws, s);
+    case kT128x128: return launch_gemm_splitk_cfg<128, 128, 4, 2, GATEUP, 2, W8>(a, p.nsplit, a.ws, s);
+    default: return launch_gemm_splitk_cfg<256, 256, 4, 2, GATEUP, 2, W8>(a, p.nsplit, a.ws, s);
   }
 }
 
-template int launch_gemm_split<false>(const StreamArgs&, const GemmSplit&, hipStream_t);
-template int launch_gemm_split<true>(const StreamArgs&, const GemmSplit&, hipStream_t);
+template int launch_gemm_split<false, false>(const StreamArgs&, const GemmSplit&, hipStream_t);
+template int launch_gemm_split<true, false>(const StreamArgs&, const GemmSplit&, hipStream_t);
+template int launch_gemm_split<false, true>(const StreamArgs&, const GemmSplit&, hipStream_t);
+template int launch_gemm_split<true, true>(const StreamArgs&, const GemmSplit&, hipStream_t);
 template int launch_gemm<false, false>(const StreamArgs&, hipStream_t);
 template int launch_gemm<true, false>(const StreamArgs&, hipStream_t);
 template int launch_gemm<false, true>(const StreamArgs&, hipStream_t);

@@ -130,7 +130,9 @@ GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup);
 int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K, bool gateup);
 // Whether the bf16 call a runs split (plan + workspace large enough).
 bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p);
-template <bool GATEUP>
+// W8: int8 weights with row scales, dequantised in registers (the partials
+// equal those of the bf16 split over the dequantised weights).
+template <bool GATEUP, bool W8>
 int launch_gemm_split(const StreamArgs& a, const GemmSplit& p, hipStream_t s);
 
 // Device-side per-row int8 quantisation.

@@ -358,7 +358,7 @@ int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
   // bf16 against large weights with a caller workspace: k split across
   // workgroups (fp_gemm.hip)
   GemmSplit sp;
-  if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP>(a, sp, s);
+  if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP, false>(a, sp, s);
   // bf16 from 3 (small N, e.g. QKV) or 8 rows: split-K tiles (fp_splitk.hip)
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
   const int64_t min_m = wrows <= kSplitkSmallN ? kSplitkMinMSmallN : kSplitkMinM;

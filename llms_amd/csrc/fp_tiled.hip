@@ -222,7 +222,7 @@ template <bool GATEUP, bool W8>
 int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
   GemmSplit sp;
-  if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP>(a, sp, s);
+  if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP, false>(a, sp, s);
   if (!W8 && a.M <= kSplitkMaxM && wrows <= kSplitkSmallN && a.K >= kSplitkMinKTiled &&
       splitk_supported(a, aligned, false) && !k128_wide(a.M, a.N, a.K, GATEUP))
     return launch_splitk<GATEUP, false>(a, s);

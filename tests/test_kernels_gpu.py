@@ -603,8 +603,9 @@ def test_split_k_across_workgroups(M, N, K, op):
                                          (600, 2560, 4352, "qkv", True)])
 def test_int8_dequantised_mfma_path(M, K, N, op, dq):
     """With enough rows the int8 calls dequantise the weights into the
-    workspace and run the bf16 path (split across workgroups where planned);
-    the contract is unchanged. Below the threshold, where the int8 split-K
+    workspace and run the bf16 path (or, where that path splits k across at
+    least 4 workgroups, run the split on the int8 weights: see
+    test_int8_split_across_workgroups); the contract is unchanged. Below the threshold, where the int8 split-K
     tiles take the shape (K % 64 == 0, up to 128 rows, K <= 8192 above 64) and
     where the int8 gemm does (gate-up up to 1024 rows, one weight stream of
     more than 4096 rows with K <= 2560 up to 512 rows), the in-register int8
@@ -632,6 +633,38 @@ def test_int8_dequantised_mfma_path(M, K, N, op, dq):
             y = kern.fused_linear_w8(x.to(DEV), q, s).cpu()
         out = ref.ref_linear_w8(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy())
     _check(y[rows], out, f"int8 {op} M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M,K,N,op", [(128, 9728, 2560, "linear"), (256, 4096, 6144, "qkv"),
+                                      (256, 4096, 2560, "linear"), (200, 12288, 1001, "linear")])
+def test_int8_split_across_workgroups(M, K, N, op):
+    """int8 calls whose bf16 plan splits k across at least 4 workgroups run
+    that split on the int8 weights, dequantising in registers: the workspace
+    is just the partials (the bf16 call's size), the result is bit-identical
+    to the bf16 split over the dequantised weights bf16(q * s) and matches the
+    oracle. Covers Qwen3 down at 128 rows, 8B QKV at 256, o at 256 and a ragged
+    narrow output."""
+    from llms_amd import _lib
+
+    lib = _lib.capi()
+    need = lib.fp_workspace_bytes_w8(M, N, K, 0)
+    assert need > 0 and need == lib.fp_workspace_bytes(M, N, K, 0)
+    kern = _kernels()
+    x, w = qkv_inputs(190 + M, M, K, N, 0)
+    q, s = _quant(w)
+    xd = x.to(DEV)
+    wdq = (q.float() * s[:, None]).to(torch.bfloat16)   # the dequantised weights
+    if op == "qkv":
+        n_k = N // 6
+        y = torch.cat(kern.fused_qkv_w8(xd, q, s, n_q=N - 2 * n_k, n_k=n_k), dim=-1)
+        yb = torch.cat(kern.triton_fused_qkv(xd, wdq, n_q=N - 2 * n_k, n_k=n_k), dim=-1)
+    else:
+        y = kern.fused_linear_w8(xd, q, s)
+        yb = kern.fused_linear(xd, wdq)
+    assert torch.equal(y.view(torch.int16), yb.view(torch.int16)), f"int8 split {op} M={M}"
+    rows = _rows(M, limit=64)
+    _check(y.cpu()[rows], ref.ref_linear_w8(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy()),
+           f"int8 split {op} M={M} K={K} N={N}")
 
 
 @pytest.mark.parametrize("M", [1, 4, 64, 2048])
