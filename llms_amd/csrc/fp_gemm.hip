@@ -444,13 +444,14 @@ bool gemm_supported(const StreamArgs& a, bool aligned, bool w8) {
 // kK*: bf16 tiles with 128-wide k-steps (two LDS stages: 64 KB, 112 KB and
 // 128 KB).
 enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256, kT192x256,
-                kK64x64, kK96x128, kK128x128 };
+                kK64x64, kK96x128, kK128x128, kT320x256 };
 struct TileInfo {
   int bn, bm, per_cu;
 };
 constexpr TileInfo kTiles[] = {{64, 32, 4},   {128, 64, 3},  {64, 128, 2},
                                {128, 128, 2}, {256, 256, 1}, {192, 256, 1},
-                               {64, 64, 2},   {96, 128, 1},  {128, 128, 1}};
+                               {64, 64, 2},   {96, 128, 1},  {128, 128, 1},
+                               {320, 256, 1}};
 constexpr int kCUs = 256;
 
 int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
@@ -481,7 +482,7 @@ int split_ref_tile(int64_t M, int64_t wrows) {
 // dispatch it yields is within 0.1% of the best of the candidates below on
 // average over those 120 shapes, 4% at worst). A grid's time is set by its busiest CU,
 // which runs k = ceil(tiles / 256) tiles; what a tile costs hardly depends on
-// how many other CUs are busy. 256 x 256 and 192 x 256 tiles (one per CU)
+// how many other CUs are busy. 256 x 256, 192 x 256 and 320 x 256 tiles (one per CU)
 // cost k times (per-k-step + per-tile) units; tiles that fit two per CU run
 // in pairs: k / 2 pairs and k % 2 single tiles, each with its own per-k-step
 // cost (a pair costs ~1.1-1.3 times a single), plus a per-tile cost. Units
@@ -495,6 +496,7 @@ constexpr TileCost kCost64x128{0.576, 0.598, 0.0};
 constexpr TileCost kCost128x128{0.616, 0.765, 1.085};
 constexpr TileCost kCost256x256{1.086, 0.0, 7.200};
 constexpr TileCost kCost192x256{0.948, 0.0, 4.843};
+constexpr TileCost kCost320x256{1.331, 0.0, 7.814};
 constexpr double kCostLaunch = 1.925;  // the tail plan's second launch
 
 double grid_cost(int tile, int64_t M, int64_t N, int64_t nkt, bool gateup) {
@@ -504,6 +506,7 @@ double grid_cost(int tile, int64_t M, int64_t N, int64_t nkt, bool gateup) {
   const TileCost& c = tile == kT64x128    ? kCost64x128
                       : tile == kT128x128 ? kCost128x128
                       : tile == kT192x256 ? kCost192x256
+                      : tile == kT320x256 ? kCost320x256
                                           : kCost256x256;
   if (kTiles[tile].per_cu == 1) return (double)k * ((double)nkt * c.single + c.tile);
   const int64_t pairs = k / 2, singles = k % 2;
@@ -513,7 +516,10 @@ double grid_cost(int tile, int64_t M, int64_t N, int64_t nkt, bool gateup) {
 
 // The unsplit plan: for bf16 weights a single round of k-step-128 tiles where
 // one fits (k128_tile); otherwise the cheapest of 64 x 128, 128 x 128,
-// 256 x 256, 192 x 256, and
+// 256 x 256, 192 x 256, 320 x 256 (bf16, at most two rounds: 11% more bytes
+// per k-step than 256 x 256 for 25% more work, which pays where it saves a
+// round: 4B gate-up M = 2048 195.6 -> 184.4 us, M = 1024 116.7 -> 99.5 us;
+// 4B QKV M = 3072 104.8 -> 83.8 us), and
 // "256 x 256 for whole rounds + a 128 x 128 tail" (nmain > 0: the first
 // nmain output columns as whole 256 x 256 rounds, the rest as 128 x 128 tiles
 // in a second launch). The tail form turns the last partial round of 256 x
@@ -567,12 +573,14 @@ int k128_tile(int64_t M, int64_t N, int64_t K, bool gateup) {
   return best;
 }
 
-// Whether a single round of k-step-128 tiles (k128_tile) has at least one
-// tile per 20 columns of K: enough tiles against the k loop that splitting k
-// (across or inside workgroups) no longer pays.
+// Whether a single round of k-step-128 tiles (k128_tile) has a tile for
+// every CU and at least one tile per 20 columns of K: enough tiles against
+// the k loop that splitting k (across or inside workgroups) no longer pays.
 bool k128_wide(int64_t M, int64_t N, int64_t K, bool gateup) {
   const int t = k128_tile(M, N, K, gateup);
-  return t >= 0 && tile_count(t, M, N, gateup) * 20 >= K;
+  if (t < 0) return false;
+  const int64_t n = tile_count(t, M, N, gateup);
+  return n >= kCUs && n * 20 >= K;
 }
 
 GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf16) {
@@ -583,7 +591,10 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf
   const int64_t nkt = K / kBK;
   GemmPlan best{kT64x128, 0};
   double cbest = grid_cost(kT64x128, M, N, nkt, gateup);
-  for (int t : {kT128x128, kT256x256, kT192x256}) {
+  for (int t : {kT128x128, kT256x256, kT192x256, kT320x256}) {
+    // 320 x 256 (bf16 only) for at most two rounds: beyond, the model
+    // underrates it by 2-4%
+    if (t == kT320x256 && (!bf16 || tile_count(t, M, N, gateup) > 2 * kCUs)) continue;
     const double c = grid_cost(t, M, N, nkt, gateup);
     if (c < cbest) best = GemmPlan{t, 0}, cbest = c;
   }
@@ -608,6 +619,9 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
   const GemmPlan p = gemm_plan_unsplit(a.M, a.N, a.K, GATEUP, !W8);
   if constexpr (!W8) {
     switch (p.tile) {
+      case kT320x256:
+        if constexpr (GATEUP) return launch_gemm_cfg<320, 256, 2, 4, true, 2>(a, s);
+        return launch_gemm_cfg<320, 256, 4, 2, false, 2>(a, s);
       case kK64x64: return launch_gemm_cfg<64, 64, 2, 2, GATEUP, 2, false, 128>(a, s);
       case kK128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, false, 128>(a, s);
       case kK96x128:
@@ -662,12 +676,13 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
 // 256 x 256 above; splits = slots / tiles rounded, in 2..16 with at least
 // 8 k-steps each. No split where a single round of k-step-128 tiles can run
 // instead (k128_tile) with K <= 4096 and either at most 3 splits, or at most
-// 6 with weights under 2^24 elements and one tile per 20 columns of K
-// (k128_wide) (measured: 4B QKV M = 256 28.6 -> 18.5 us, 4B o M = 640
-// 35.1 -> 26.6 us, 8B o M = 1024 49.4 -> 47.8 us, 0.6B o M = 1024 20.9 ->
-// 14.3 us; with 8 splits, 4-5 over 8B QKV and o weights, or rounds of few
-// tiles against K, such as 0.6B o and down below 256 rows, the split is
-// 5-36% faster).
+// 5 with weights under 2^24 elements and a wide round (k128_wide)
+// (measured on two MI355X boxes: 4B QKV M = 256 28.6 -> 18.5-24.4 us, 4B o
+// M = 640 35.2 -> 26.6-32.7 us, 8B o M = 1024 49.4-50.0 -> 47.8-48.4 us;
+// with 6-8 splits, 4-5 over 8B QKV and o weights, or rounds of few tiles
+// against K, such as 0.6B o and down below 256 rows, the split is up to 36%
+// faster; 4B o at 448-512 rows, 6 splits, ran 26 us split on both boxes and
+// 26 or 31-34 us as a single round).
 GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
   const GemmSplit none{-1, 1};
   if (M < 32 || K % kBK != 0) return none;
@@ -694,7 +709,7 @@ GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (ns < 2) return none;
   const int used = gemm_splitk_used(K, (int)ns);
   if (K <= 4096 && k128_tile(M, N, K, gateup) >= 0 &&
-      (used <= 3 || (used <= 6 && wrows * K < ((int64_t)1 << 24) && k128_wide(M, N, K, gateup))))
+      (used <= 3 || (used <= 5 && wrows * K < ((int64_t)1 << 24) && k128_wide(M, N, K, gateup))))
     return none;
   return GemmSplit{tile, used};
 }

@@ -116,7 +116,8 @@ struct GemmPlan {
 };
 GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf16);
 // Whether the bf16 plan is a single round of tiles with 128-wide k-steps with
-// at least one tile per 20 columns of K (then it beats the split-K tiles).
+// a tile for every CU and one per 20 columns of K (then it beats the split-K
+// tiles).
 bool k128_wide(int64_t M, int64_t N, int64_t K, bool gateup);
 // k split across workgroups — for calls whose tile grid leaves the chip
 // partly idle while each tile has a long k loop — with fp32 partials in the

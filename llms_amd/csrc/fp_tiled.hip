@@ -212,9 +212,10 @@ int launch_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // to kSplitkMaxM rows against at most 8192 weight rows with K >=
 // kSplitkMinKTiled, which give too few tiles for 256 CUs and run the
 // in-workgroup split-K tiles, unless a round of tiles with 128-wide k-steps
-// has one tile per 20 columns of K (k128_wide: Qwen3-4B QKV, 6144 x 2560, at
-// 65-256 rows: 17.6-33.3 -> 16.9-18.5 us; 8B QKV below 160 rows, 4B o and
-// 0.6B o and down keep the split-K tiles, 5-20% faster there). int8 shapes that
+// has a tile for every CU and one per 20 columns of K (k128_wide: Qwen3-4B
+// QKV, 6144 x 2560, at 160-256 rows: 23.0-28.6 -> 17.9-24.4 us; below 160
+// rows, and 8B QKV, 4B o and 0.6B o and down, keep the split-K tiles, up to
+// 20% faster there). int8 shapes that
 // splitk8_shape() admits run the split-K tiles too, other aligned int8 calls
 // with whole 64-wide k-steps run gemm_kernel (both dequantise in registers);
 // unaligned rows and K tails run tiled_kernel.

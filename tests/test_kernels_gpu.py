@@ -285,16 +285,16 @@ def test_qwen3_4b_prefill_8192_rows():
 
 
 # Row counts whose prefill grids differ. Qwen3-4B: 64 x 64 tiles with
-# 128-wide k-steps (QKV 96 and 256 rows), 96 x 128 (QKV 384) and 128 x 128
+# 128-wide k-steps (QKV 160 and 256 rows), 96 x 128 (QKV 384) and 128 x 128
 # (QKV 640) with 128-wide k-steps, 64 x 128 (gate-up 128 rows), 128 x 128
-# (gate-up 384, QKV 768), 192 x 256 (gate-up 512, QKV 1536 and 2048) and
-# 256 x 256 tiles (gate-up 1536), and whole 256 x 256 rounds followed by a
-# 128 x 128 tail launch (gate-up 1024 and 2048, QKV 3072). Qwen3-0.6B: 64 x 64
-# (gate-up 96 and 320, QKV 128) and 128 x 128 (gate-up 512, QKV 640) with
-# 128-wide k-steps, 128 x 128 (gate-up 1024, QKV 1536 and 3072) and 192 x 256
-# (gate-up 2048).
+# (gate-up 384, QKV 768), 192 x 256 (gate-up 512, QKV 1536 and 2048),
+# 256 x 256 (gate-up 1536) and 320 x 256 tiles (gate-up 1024 and 2048, QKV
+# 3072), and whole 256 x 256 rounds followed by a 128 x 128 tail launch (QKV
+# 4096). Qwen3-0.6B: 64 x 64 (gate-up 96 and 320, QKV 128) and 128 x 128
+# (gate-up 512, QKV 640) with 128-wide k-steps, 128 x 128 (gate-up 1024, QKV
+# 1536 and 3072) and 192 x 256 (gate-up 2048).
 PLAN_ROWS = {"gate_up": (QWEN3_4B, 2048, [128, 384, 512, 1024, 1536]),
-             "qkv": (QWEN3_4B, 3072, [96, 256, 384, 640, 768, 1536, 2048]),
+             "qkv": (QWEN3_4B, 4096, [160, 256, 384, 640, 768, 1536, 2048, 3072]),
              "gate_up_0.6b": (QWEN3_0_6B, 2048, [96, 320, 512, 1024]),
              "qkv_0.6b": (QWEN3_0_6B, 3072, [128, 640, 1536])}
 
