@@ -556,6 +556,27 @@ def test_linear_tails(M, K, N):
     check_linear(120 + M, M, K, N)
 
 
+@pytest.mark.parametrize("op,M,K,N", [
+    ("linear", 200, 1024, 1001),    # 64 x 64, 128-wide k-steps; odd N: scalar stores
+    ("gate-up", 150, 1024, 1000),   # 64 x 64 gate-up, ragged M and N
+    ("gate-up", 500, 1024, 3000),   # 128 x 128, 128-wide k-steps, ragged
+    ("qkv", 384, 1024, 6144),       # 96 x 128, 128-wide k-steps
+    ("qkv", 250, 2560, 4800),       # 64 x 64, ragged M
+    ("gate-up", 1000, 1024, 9728),  # 320 x 256 gate-up, partial last tiles
+    ("qkv", 3000, 1024, 6144)])     # 320 x 256, partial last tiles
+def test_wide_k_and_320_tiles_ragged(op, M, K, N):
+    """Ragged calls on the tiles with 128-wide k-steps and on 320 x 256 tiles
+    (which tile runs is the planner's choice for these shapes): partial tiles
+    in M and N, odd output widths, against the oracle."""
+    if op == "linear":
+        check_linear(200 + M, M, K, N)
+    elif op == "gate-up":
+        check_ffn(210 + M, M, K, N)
+    else:
+        n_k = N // 6
+        check_qkv(220 + M, M, K, N - 2 * n_k, n_k)
+
+
 @pytest.mark.parametrize("M,N,K,op", [
     (32, 2560, 9728, "linear"), (100, 4096, 12288, "linear"), (300, 1001, 8192, "linear"),
     (1024, 2560, 9728, "linear"), (2048, 2560, 9728, "linear"), (256, 6144, 4096, "qkv"),
