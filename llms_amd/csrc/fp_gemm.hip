@@ -530,6 +530,7 @@ double grid_cost(int tile, int64_t M, int64_t N, int64_t nkt, bool gateup) {
 // the model: where 128 x 128 tiles would run one per CU and 64 x 128 tiles at
 // most two, 64 x 128 is faster on every shape measured (the pair of smaller
 // tiles hides latency better than one tile of the same work).
+//
 // Grids of tiles with 128-wide k-steps: twice the bytes per load round and
 // half the per-step waits and barriers of the 64-wide tiles. Measured on
 // MI355X (Qwen3-0.6B/4B/8B QKV, o, down and gate-up, M = 160..2048; results
