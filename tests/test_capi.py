@@ -321,3 +321,54 @@ def test_int8_entry_points_without_workspace_prefill():
         torch.cuda.synchronize()
         p = ref.check_parity(bits(y.cpu())[r], out())
         assert p.ok, (kind, M, p)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,M,K,N", [("qkv", 384, 1024, 6144),      # 96 x 128, 128-wide k-steps
+                                        ("linear", 200, 1024, 1001),   # 64 x 64, 128-wide k-steps
+                                        ("gate-up", 500, 1024, 3000),  # 128 x 128, 128-wide k-steps
+                                        ("qkv", 3000, 1024, 6144)])    # 320 x 256
+def test_padded_strides_on_prefill_tiles(kind, M, K, N):
+    """Row strides larger than the rows (ldx = K + 64, ldw = K + 128, ldy =
+    N + 8) through the C ABI on the prefill tiles: operands are addressed by
+    stride, padding is never read or written."""
+    from llms_amd import _lib
+
+    lib = _lib.capi()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ldx, ldw, ldy = K + 64, K + 128, N + 8
+    if kind == "gate-up":
+        x, wg, wu = ffn_inputs(800 + M, M, K, N)
+        mats = [wg, wu]
+    else:
+        x, w = qkv_inputs(800 + M, M, K, N, 0)
+        mats = [w]
+    xs = torch.full((M, ldx), 7.0, dtype=torch.bfloat16, device="cuda")
+    xs[:, :K] = x.cuda()
+    ws = []
+    for m in mats:
+        t = torch.full((N, ldw), 7.0, dtype=torch.bfloat16, device="cuda")
+        t[:, :K] = m.cuda()
+        ws.append(t)
+    y = torch.full((M, ldy), 3.0, dtype=torch.bfloat16, device="cuda")
+    if kind == "gate-up":
+        st = lib.fp_gate_up_silu_bf16(_p(xs), ldx, _p(ws[0]), ldw, _p(ws[1]), ldw, _p(y), ldy,
+                                      M, N, K, stream)
+    elif kind == "qkv":
+        n_k = N // 6
+        st = lib.fp_qkv_bf16(_p(xs), ldx, _p(ws[0]), ldw, _p(y), ldy, M, N - 2 * n_k, n_k, K, stream)
+    else:
+        st = lib.fp_linear_bf16(_p(xs), ldx, _p(ws[0]), ldw, _p(y), ldy, M, N, K, stream)
+    assert st == 0, _lib.status_string(st)
+    torch.cuda.synchronize()
+    yc = y.cpu()
+    assert torch.all(yc[:, N:] == 3.0), "output padding written"
+    r = np.sort(np.random.default_rng(5).choice(M, min(M, 96), replace=False))
+    if kind == "gate-up":
+        out = ref.ref_gate_up_silu_full(bits(x)[r], bits(wg), bits(wu))
+    elif kind == "qkv":
+        out = ref.ref_qkv_full(bits(x)[r], bits(w), N - 2 * (N // 6), N // 6)
+    else:
+        out = ref.ref_linear(bits(x)[r], bits(w))
+    p = ref.check_parity(bits(yc[:, :N].contiguous())[r], out)
+    assert p.ok, (kind, M, p)
