@@ -208,10 +208,11 @@ def cpu_baseline(shape, M: int, sets: int, reps: int) -> dict:
     }
 
 
-def counters_run(torch, kern, shape, layers: int) -> dict:
+def counters_run(torch, kern, shape, layers: int, Mp: int = 2048) -> dict:
     """A short fixed sequence for `rocprofv3 --pmc` runs: a plain device copy
     of known size (calibrates FETCH_SIZE / WRITE_SIZE), then the decode (M=1)
-    and prefill (M=2048) fused kernels over `layers` cycled weight sets."""
+    and prefill (M=Mp, default 2048) fused kernels over `layers` cycled weight
+    sets."""
     K, n_q, n_k, inter = shape
     n_qkv = n_q + 2 * n_k
     copy_bytes = 256 << 20
@@ -224,7 +225,7 @@ def counters_run(torch, kern, shape, layers: int) -> dict:
     torch.cuda.synchronize()
     run_step(stack, kern)
     torch.cuda.synchronize()
-    stack.set_m(torch, 2048)
+    stack.set_m(torch, Mp)
     for l in range(min(4, layers)):
         kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k)
         kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l])
@@ -237,10 +238,10 @@ def counters_run(torch, kern, shape, layers: int) -> dict:
                        "launches": layers},
         "qkv_m1": {"read_bytes": 2 * K * n_qkv + 2 * K, "write_bytes": 2 * n_qkv,
                    "launches": layers},
-        "gate_up_m2048": {"read_bytes": 2 * K * 2 * inter + 2 * 2048 * K,
-                          "write_bytes": 2 * 2048 * inter, "launches": min(4, layers)},
-        "qkv_m2048": {"read_bytes": 2 * K * n_qkv + 2 * 2048 * K,
-                      "write_bytes": 2 * 2048 * n_qkv, "launches": min(4, layers)},
+        f"gate_up_m{Mp}": {"read_bytes": 2 * K * 2 * inter + 2 * Mp * K,
+                           "write_bytes": 2 * Mp * inter, "launches": min(4, layers)},
+        f"qkv_m{Mp}": {"read_bytes": 2 * K * n_qkv + 2 * Mp * K,
+                       "write_bytes": 2 * Mp * n_qkv, "launches": min(4, layers)},
     }
 
 
@@ -446,7 +447,7 @@ def main() -> int:
     n_qkv = n_q + 2 * n_k
     L = args.layers
     if args.counters:
-        print(json.dumps(counters_run(torch, kern, shape, L)), flush=True)
+        print(json.dumps(counters_run(torch, kern, shape, L, args.prefill_m)), flush=True)
         return 0
     if args.decode:
         print(json.dumps(decode_run(torch, args.decode_tokens)), flush=True)
