@@ -107,3 +107,43 @@ def test_graph_greedy_generate_tokens():
     same = next((i for i, (a, b) in enumerate(zip(te, tg)) if a != b), len(te))
     print(f"\neager {te}\ngraph {tg}")
     assert same >= 8, (te, tg)
+
+
+@pytest.mark.gpu
+def test_prefill_calls_replay_in_graph():
+    """Prefill-sized calls captured in one HIP graph — QKV on 96 x 128 tiles
+    with 128-wide k-steps (384 rows), gate-up on 320 x 256 tiles (2048 rows),
+    a down projection split across workgroups (fp32 partials in a workspace
+    from the graph's pool, then the reduce) and an int8 down projection split
+    the same way — replay bit-identically to the eager calls, several times,
+    with eager work between the replays."""
+    from llms_amd import kernels as K
+    from tests._util import ffn_inputs, qkv_inputs
+
+    xq, wq = qkv_inputs(31, 384, 2560, 4096, 1024)
+    xg, wg, wu = ffn_inputs(32, 2048, 2560, 9728)
+    xd, wdn = qkv_inputs(33, 512, 9728, 2560, 0)
+    xq, wq, xg, wg, wu, xd, wdn = (t.to(DEV) for t in (xq, wq, xg, wg, wu, xd, wdn))
+    q8, s8 = K.quantize_w8_per_row(wdn)
+
+    def calls():
+        q, k, v = K.triton_fused_qkv(xq, wq, n_q=4096, n_k=1024)
+        return [q, k, v, K.triton_fused_gate_up_silu(xg, wg, wu),
+                K.fused_linear(xd, wdn), K.fused_linear_w8(xd, q8, s8)]
+
+    eager = [t.clone() for t in calls()]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls()                      # warm the allocator outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = calls()
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, eager)):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (rep, i)
+        _ = (xq.float() @ wq[:64].float().t()).sum().item()   # eager work between replays
