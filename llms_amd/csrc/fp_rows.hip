@@ -25,8 +25,8 @@
 // torch rounding points, and one 2-byte store: no LDS reduction, no barrier
 // after the prologue.
 // x (MM rows of K bf16, zero beyond M) is staged once per workgroup in LDS
-// while the wave's first weight loads are in flight — except one bf16 row
-// with K <= 2560, which each lane reads from L2 chunk by chunk along with the
+// while the wave's first weight loads are in flight — except one row with
+// K <= 2560, which each lane reads from L2 chunk by chunk along with the
 // weights (no staging, no barrier).
 // Requirements (checked by rows_supported): M <= kRowsMaxM, 16-byte-aligned
 // rows with K % 8 == 0 (int8: K % 16 == 0), staged x within kRowsMaxLds.
@@ -54,12 +54,13 @@ __device__ __forceinline__ float diag(f32x4 d, int lane) {
 
 // NW waves per workgroup, R rows per wave, U weight chunks in flight per wave,
 // MM x rows (the call's M rounded up; the extra rows are zeros in LDS). NORM:
-// x is RMS-normalised (a.gamma, a.eps) on its way into LDS. XG (one bf16 x
-// row, no norm): no LDS staging and no barrier; each lane loads its 16 bytes
-// of x for a chunk from global memory (L2) together with the chunk's weights.
+// x is RMS-normalised (a.gamma, a.eps) on its way into LDS. XG (one x row, no
+// norm): no LDS staging and no barrier; each lane loads its 16 bytes (int8:
+// 32 bytes) of x for a chunk from global memory (L2) together with the
+// chunk's weights.
 template <int NW, int R, int U, int MM, bool GATEUP, bool W8, bool NORM, bool XG = false>
 __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
-  static_assert(!XG || (MM == 1 && !W8 && !NORM), "x from global memory: one bf16 row");
+  static_assert(!XG || (MM == 1 && !NORM), "x from global memory: one row, no norm");
   constexpr int KC = kc<W8>();
   constexpr int KL = KC / kWave;  // k elements per lane per chunk
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -73,13 +74,16 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   const int T = nr * J;  // chunks of this wave
 
   // Weight chunks are consumed in issue order: chunk t sits in slot t % U.
-  u32x4 wg[U], wu[U], xg[XG ? U : 1];
+  u32x4 wg[U], wu[U], xg[XG ? U : 1], xg1[XG && W8 ? U : 1];
   int ir = 0, ij = 0;  // (row, chunk) of the next chunk to issue
   auto issue = [&](int u) {
     if (ir < nr) {
       const int64_t row = row0 + ir;
       const int64_t k = (int64_t)ij * KC + KL * lane;
-      if constexpr (XG) xg[u] = load_bf16x8<true>(a.x, k, K);
+      if constexpr (XG) {
+        xg[u] = load_bf16x8<true>(a.x, k, K);
+        if constexpr (W8) xg1[u] = load_bf16x8<true>(a.x, k + 8, K);
+      }
       if constexpr (W8) {
         wg[u] = load_i8x16<true>((const int8_t*)a.w0 + row * a.ldw0, k, K);
         if constexpr (GATEUP) wu[u] = load_i8x16<true>((const int8_t*)a.w1 + row * a.ldw1, k, K);
@@ -192,8 +196,14 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
           }
 #pragma unroll
           for (int m = 0; m < MM; ++m) {
-            const u32x4 xv = *reinterpret_cast<const u32x4*>(xp + m * Kp);
-            const u32x4 xv1 = *reinterpret_cast<const u32x4*>(xp + m * Kp + 8);
+            u32x4 xv, xv1;
+            if constexpr (XG) {
+              xv = xg[u];
+              xv1 = xg1[u];
+            } else {
+              xv = *reinterpret_cast<const u32x4*>(xp + m * Kp);
+              xv1 = *reinterpret_cast<const u32x4*>(xp + m * Kp + 8);
+            }
             dg[m] = mfma16(g0, xv, dg[m]);
             dg[m] = mfma16(g1, xv1, dg[m]);
             if constexpr (GATEUP) {
@@ -247,11 +257,13 @@ int launch_rows_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t per = (int64_t)NW * R;
   const size_t shm = (size_t)rows_lds_bytes<W8>(MM, a.K, a.gamma != nullptr);
   const dim3 grid((unsigned)((a.N + per - 1) / per)), block(NW * kWave);
-  // One bf16 x row with K <= 2560: x straight from L2 into registers instead
-  // of an LDS copy behind a barrier (measured on MI355X, bit-identical: 4B
+  // One x row with K <= 2560: x straight from L2 into registers instead of
+  // an LDS copy behind a barrier (measured on MI355X, bit-identical: bf16 4B
   // QKV 7.46 -> 7.16 us, gate-up 18.20 -> 17.93 us, 0.6B QKV 3.85 -> 3.61 us,
-  // gate-up 5.00 -> 4.68 us; at K = 4096 (8B) it is even or 0.8% slower).
-  if constexpr (MM == 1 && !W8) {
+  // gate-up 5.00 -> 4.68 us; int8 4B QKV 6.01 -> 5.73 us, gate-up 13.7-13.9
+  // -> 13.34 us, 0.6B QKV 3.53 -> 3.22 us; at K = 4096 (8B) it is even, or
+  // for int8 gate-up 5% slower).
+  if constexpr (MM == 1) {
     if (!a.gamma && a.K <= 2560) {
       hipLaunchKernelGGL((rows_kernel<NW, R, U, MM, GATEUP, W8, false, true>), grid, block, 0, s, a);
       return (int)hipGetLastError();
