@@ -73,10 +73,15 @@ class Stack:
         self.wqkv = [w(self.n_qkv) for _ in range(layers)]
         self.wg = [w(inter) for _ in range(layers)]
         self.wu = [w(inter) for _ in range(layers)]
-        self.set_m(torch, M, g)
+        self.set_m(torch, M, seed=seed)
 
-    def set_m(self, torch, M: int, g=None):
+    def set_m(self, torch, M: int, g=None, seed=None):
+        """New x rows for M; with `seed`, drawn from a fresh generator of that
+        seed (the rows of a Stack built with it, when M matches)."""
         self.M = M
+        if seed is not None:
+            g = torch.Generator(device="cuda")
+            g.manual_seed(seed + 1)
         self.x_attn = torch.randn(M, self.K, generator=g, device="cuda").to(torch.bfloat16)
         self.x_ffn = torch.randn(M, self.K, generator=g, device="cuda").to(torch.bfloat16)
 
@@ -155,27 +160,33 @@ def profiled_traffic(path: str = TRAFFIC_PROFILE):
     return None
 
 
-def cpu_baseline(shape, M: int, sets: int, reps: int) -> dict:
-    """The reference's unfused torch path (oracle.torch_path) on the host CPU,
-    bf16, a bounded sample: `sets` distinct layer weight sets cycled."""
-    import torch
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
+
+def cpu_threads() -> int:
+    """The job's CPU share: the affinity mask, capped by OMP_NUM_THREADS
+    (set to the box's per-job share)."""
+    aff = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", aff) or aff)
+    return max(1, min(aff, share))
+
+
+def cpu_time_pair(torch, shape, x1, x2, W, reps: int) -> float:
+    """Median seconds per (QKV, gate-up) layer pair of the reference's
+    unfused torch path (oracle.torch_path) on the host CPU, cycling the
+    weight sets W in order, after one warm-up pass."""
     from oracle import torch_path as tp
 
     K, n_q, n_k, inter = shape
-    aff = len(os.sched_getaffinity(0))
-    share = int(os.environ.get("OMP_NUM_THREADS", aff) or aff)
-    threads = max(1, min(aff, share))
-    torch.set_num_threads(threads)
-    g = torch.Generator()
-    g.manual_seed(1)
-    bf = torch.bfloat16
-    x1 = torch.randn(M, K, generator=g).to(bf)
-    x2 = torch.randn(M, K, generator=g).to(bf)
-    W = [((torch.randn(n_q + 2 * n_k, K, generator=g) * 0.02).to(bf),
-          (torch.randn(inter, K, generator=g) * 0.02).to(bf),
-          (torch.randn(inter, K, generator=g) * 0.02).to(bf)) for _ in range(sets)]
-    for wq, wg, wu in W[:2]:  # warmup
+    for wq, wg, wu in W:  # warm-up pass
         tp.torch_qkv(x1, wq, n_q, n_k)
         tp.torch_gate_up_silu(x2, wg, wu)
     times = []
@@ -184,27 +195,40 @@ def cpu_baseline(shape, M: int, sets: int, reps: int) -> dict:
         for wq, wg, wu in W:
             tp.torch_qkv(x1, wq, n_q, n_k)
             tp.torch_gate_up_silu(x2, wg, wu)
-        times.append((time.perf_counter() - t0) / sets)
-    per_pair = statistics.median(times)
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for ln in f:
-                if ln.startswith("model name"):
-                    model = ln.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    gbs = pair_bytes(M, K, n_q + 2 * n_k, inter) / per_pair / 1e9
+        times.append((time.perf_counter() - t0) / len(W))
+    return statistics.median(times)
+
+
+def cpu_baseline(torch, stacks: dict, reps: int) -> dict:
+    """The reference's unfused bf16 torch path on the host CPU for each
+    {config name: (shape, Stack)}: the inputs are the GPU run's own (the
+    Stack's x rows and its layer weight sets, generated on the device from
+    the same seed and copied to the host), every weight set cycled once per
+    pass, median of `reps` passes. The first entry is the reported value."""
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    per = {}
+    for name, (shape, stack) in stacks.items():
+        K, n_q, n_k, inter = shape
+        x1, x2 = stack.x_attn.cpu(), stack.x_ffn.cpu()
+        W = [(a.cpu(), b.cpu(), c.cpu()) for a, b, c in zip(stack.wqkv, stack.wg, stack.wu)]
+        sec = cpu_time_pair(torch, shape, x1, x2, W, reps)
+        per[name] = {"gbs": round(pair_bytes(stack.M, K, n_q + 2 * n_k, inter) / sec / 1e9, 2),
+                     "ms_per_layer_pair": round(sec * 1e3, 4), "M": stack.M,
+                     "weight_sets": len(W)}
+        del W
+    first = next(iter(per))
     return {
-        "value": round(gbs, 2),
+        "value": per[first]["gbs"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/torch_path.py unfused bf16 torch path (F.linear+split, "
-                   f"F.silu(F.linear)*F.linear) on CPU, Qwen3-4B shapes M={M}, {sets} distinct "
-                   f"layer weight sets cycled, median of {reps} passes; "
-                   f"{per_pair * 1e3:.2f} ms per layer pair; cpu: {model}"),
+        "sample": (f"oracle/torch_path.py, the reference's unfused bf16 torch path "
+                   f"(F.linear+split, F.silu(F.linear)*F.linear) on the host CPU with the GPU "
+                   f"run's inputs (device-generated from seed 0, copied to the host), every "
+                   f"layer weight set cycled once per pass, median of {reps} passes; value = "
+                   f"{first}; cpu: {cpu_model()}"),
+        "configs": per,
     }
 
 
@@ -334,6 +358,75 @@ def linear_run(torch, kern, M: int, N: int, K: int, reps: int) -> dict:
             "hipblaslt_us": round(ref * 1e6, 2)}
 
 
+def _median_event_us(torch, fn, warmup: int, iters: int) -> float:
+    """The reference microbench's timer (src/bench/microbench_fused_qkv.py
+    _time_fn): `warmup` calls, then one pair of HIP events around each of
+    `iters` calls on the current stream, median in microseconds."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for i in range(iters):
+        st[i].record()
+        fn()
+        en[i].record()
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) * 1e3 for a, b in zip(st, en))
+
+
+def ship_gate_run(torch, kern, warmup: int = 50, iters: int = 200) -> dict:
+    """The reference's microbench ship gate on the Qwen3-4B shapes at M in
+    {1, 5, 8} (tests/test_kernels_fused_qkv.py:286-311,
+    tests/test_kernels_fused_ffn.py:238-265; inputs as in
+    src/bench/microbench_fused_{qkv,ffn}.py: torch.manual_seed(0), randn bf16
+    on the device). QKV: the fused call against eager_3_linears (the formal
+    gate) and eager_concat_linear (one F.linear over [Wq; Wk; Wv] + split,
+    informational). Gate-up: the fused call against eager
+    silu(x Wg^T) * (x Wu^T). pass: fused median <= the gate's median, the
+    reference's criterion."""
+    import torch.nn.functional as F
+
+    K, n_q, n_k, inter = SHAPES["qwen3-4b"]
+    bf = torch.bfloat16
+    out = {"mode": "ship_gate", "shape": "qwen3-4b", "warmup": warmup, "iters": iters,
+           "timer": "median of per-call HIP events (reference microbench method)",
+           "qkv": {}, "gate_up": {}}
+    for M in (1, 5, 8):
+        torch.manual_seed(0)
+        x = torch.randn(M, K, device="cuda", dtype=bf)
+        Wq = torch.randn(n_q, K, device="cuda", dtype=bf)
+        Wk = torch.randn(n_k, K, device="cuda", dtype=bf)
+        Wv = torch.randn(n_k, K, device="cuda", dtype=bf)
+        W = torch.cat([Wq, Wk, Wv], dim=0).contiguous()
+        e3 = _median_event_us(torch, lambda: (F.linear(x, Wq), F.linear(x, Wk), F.linear(x, Wv)),
+                              warmup, iters)
+        ec = _median_event_us(torch, lambda: F.linear(x, W).split([n_q, n_k, n_k], dim=-1),
+                              warmup, iters)
+        fu = _median_event_us(torch, lambda: kern.triton_fused_qkv(x, W, n_q=n_q, n_k=n_k),
+                              warmup, iters)
+        out["qkv"][f"M={M}"] = {"eager_3_linears_us": round(e3, 2),
+                                "eager_concat_linear_us": round(ec, 2),
+                                "fused_us": round(fu, 2),
+                                "speedup_vs_3_linears": round(e3 / fu, 3),
+                                "speedup_vs_concat": round(ec / fu, 3),
+                                "pass": fu <= e3}
+        del Wq, Wk, Wv, W
+        torch.manual_seed(0)
+        x = torch.randn(M, K, device="cuda", dtype=bf)
+        Wg = torch.randn(inter, K, device="cuda", dtype=bf)
+        Wu = torch.randn(inter, K, device="cuda", dtype=bf)
+        ee = _median_event_us(torch, lambda: F.silu(F.linear(x, Wg)) * F.linear(x, Wu),
+                              warmup, iters)
+        fu = _median_event_us(torch, lambda: kern.triton_fused_gate_up_silu(x, Wg, Wu),
+                              warmup, iters)
+        out["gate_up"][f"M={M}"] = {"eager_us": round(ee, 2), "fused_us": round(fu, 2),
+                                    "speedup": round(ee / fu, 3), "pass": fu <= ee}
+        del Wg, Wu
+    out["pass"] = all(v["pass"] for d in (out["qkv"], out["gate_up"]) for v in d.values())
+    return out
+
+
 # Every configuration BASELINE.json lists: (model, M, int8).
 CONFIGS = ([("qwen3-0.6b", 1, False)]
            + [("qwen3-4b", m, False) for m in (1, 3, 4, 8, 512, 2048, 8192)]
@@ -407,7 +500,6 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--model", default="qwen3-4b", choices=sorted(SHAPES))
     ap.add_argument("--prefill-m", type=int, default=2048)
-    ap.add_argument("--cpu-sets", type=int, default=8)
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -421,6 +513,9 @@ def main() -> int:
     ap.add_argument("--configs", action="store_true",
                     help="time both projections on every BASELINE configuration (with "
                          "hipBLASLt for scale); one JSON line per configuration")
+    ap.add_argument("--ship-gate", action="store_true",
+                    help="the reference's microbench ship gate (fused <= eager at M = 1, 5, 8 "
+                         "on Qwen3-4B QKV and gate-up); prints one JSON line")
     ap.add_argument("--linear", metavar="M,N,K",
                     help="time only the plain projection (down / o) of this shape over "
                          "cycled weight sets and print one JSON line (profiling aid)")
@@ -454,6 +549,9 @@ def main() -> int:
         return 0
     if args.configs:
         configs_run(torch, kern, args.steps)
+        return 0
+    if args.ship_gate:
+        print(json.dumps(ship_gate_run(torch, kern)), flush=True)
         return 0
     if args.linear:
         M, N, Kl = (int(v) for v in args.linear.split(","))
@@ -519,14 +617,21 @@ def main() -> int:
         log(f"prefill M={Mp}: {prefill}")
         del graph
 
-    del stack
-    torch.cuda.empty_cache()
-
     cpu = None
     if not args.no_cpu:
+        # BASELINE configs 1 (this run's decode workload, M = 1) and 0
+        # (Qwen3-0.6B, M = 1), on the same device-generated inputs
         log("timing the CPU baseline")
-        cpu = cpu_baseline(shape, 1, args.cpu_sets, args.cpu_reps)
-        log(f"cpu: {cpu['value']} GB/s on {cpu['cores']} threads")
+        stack.set_m(torch, 1, seed=0)
+        small = Stack(torch, SHAPES["qwen3-0.6b"], L, M=1)
+        cpu = cpu_baseline(torch, {f"{args.model} M=1": (shape, stack),
+                                   "qwen3-0.6b M=1": (SHAPES["qwen3-0.6b"], small)},
+                           args.cpu_reps)
+        del small
+        log(f"cpu: {cpu['value']} GB/s on {cpu['cores']} threads ({cpu['configs']})")
+
+    del stack
+    torch.cuda.empty_cache()
 
     out = {
         "metric": METRIC,

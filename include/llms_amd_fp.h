@@ -213,11 +213,14 @@ int fp_linear_w8_ws(const void* x, int64_t ldx,
  *   xn[k] = bf16(gamma[k] * bf16(x[k] * r))
  * and then the contract of the matching projection on xn. Decode-sized calls
  * (the row-streaming regime: bf16 M <= 2, int8 M <= 4, with room for x in
- * LDS) run as one launch that normalises x while staging it; the others need
- * fp_rmsnorm_workspace_bytes(M, N, K, gate_up, int8) bytes of workspace
+ * LDS) whose x, weights and gamma are 16-byte aligned with row strides that
+ * are multiples of 8 (int8 weights: 16) run as one launch that normalises x
+ * while staging it and need no workspace. Every other call needs a workspace
  * (the normalised rows, then any split-k partials, or for int8 calls with
- * enough rows the dequantised weights as in fp_qkv_w8_ws) and return
- * FP_ERR_WORKSPACE without it. eps must be finite and >= 0.
+ * enough rows the dequantised weights as in fp_qkv_w8_ws) and returns
+ * FP_ERR_WORKSPACE without one; fp_rmsnorm_workspace_bytes(M, N, K, gate_up,
+ * int8) is enough for any pointers and strides of that shape. eps must be
+ * finite and >= 0.
  */
 int64_t fp_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up, int int8);
 

@@ -349,9 +349,13 @@ int fp_linear_w8_ws(const void* x, int64_t ldx, const int8_t* q, int64_t ldq, co
 int64_t fp_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up, int int8) {
   if (M < 1 || N < 1 || K < 1) return 0;
   const bool w8 = int8 != 0;
-  if (M <= (w8 ? fp::kRowsMaxM : 2) && K % (w8 ? 16 : 8) == 0 && fp::rows_fit(M, K, w8, true))
-    return 0;
+  // Room for the normalised rows always: decode-sized calls usually run as
+  // one launch and leave it unused, but take the two-launch path when a
+  // pointer or stride misses the 16-byte alignment of that launch. There the
+  // plain dispatch (bf16 M <= 2, int8 M <= 4) needs no further workspace.
   int64_t b = fp::round_up(M * K * 2, 256);
+  if (M <= (w8 ? fp::kRowsMaxM : 2) && K % (w8 ? 16 : 8) == 0 && fp::rows_fit(M, K, w8, true))
+    return b;
   if (w8) return b + fp::w8_workspace_bytes(M, N, K, gate_up != 0);
   return b + 4 * fp::gemm_split_ws_floats(fp::gemm_split_plan(M, N, K, gate_up != 0), M, N, K,
                                           gate_up != 0);

@@ -431,7 +431,6 @@ int launch_gemm_splitk_cfg(const StreamArgs& a, int nsplit, float* ws, hipStream
   return (int)hipGetLastError();
 }
 
-#ifndef FP_GEMM_NO_DISPATCH
 // Whether gemm_kernel can run this call: whole 64-wide k-steps, 16-byte
 // aligned rows, every operand's byte size below 2^31 (buffer-resource sizes
 // and 32-bit lane offsets); int8 also needs its row scales.
@@ -751,6 +750,5 @@ template int launch_gemm<false, false>(const StreamArgs&, hipStream_t);
 template int launch_gemm<true, false>(const StreamArgs&, hipStream_t);
 template int launch_gemm<false, true>(const StreamArgs&, hipStream_t);
 template int launch_gemm<true, true>(const StreamArgs&, hipStream_t);
-#endif
 
 }  // namespace fp

@@ -258,7 +258,6 @@ int launch_splitk_cfg(const StreamArgs& a, hipStream_t s) {
 
 }  // namespace
 
-#ifndef FP_SPLITK_NO_DISPATCH
 bool splitk_supported(const StreamArgs& a, bool aligned, bool w8) {
   constexpr int64_t kLim = (int64_t)1 << 31;
   const int64_t wb = w8 ? 1 : 2;
@@ -303,6 +302,5 @@ template int launch_splitk<false, false>(const StreamArgs&, hipStream_t);
 template int launch_splitk<true, false>(const StreamArgs&, hipStream_t);
 template int launch_splitk<false, true>(const StreamArgs&, hipStream_t);
 template int launch_splitk<true, true>(const StreamArgs&, hipStream_t);
-#endif
 
 }  // namespace fp

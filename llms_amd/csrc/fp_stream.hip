@@ -343,7 +343,6 @@ int launch_stream_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 
 }  // namespace
 
-#ifndef FP_STREAM_NO_DISPATCH
 // Configurations measured on MI355X (Qwen3-4B shapes, 36 cycled weight sets):
 // 4 waves per 8-row tile with interleaved k-blocks; packed x for M <= 8; the
 // gate-up kernel (two weight streams) keeps 4 k-blocks per buffer in flight,
@@ -377,6 +376,5 @@ template int launch_stream<false, false>(const StreamArgs&, bool, hipStream_t);
 template int launch_stream<true, false>(const StreamArgs&, bool, hipStream_t);
 template int launch_stream<false, true>(const StreamArgs&, bool, hipStream_t);
 template int launch_stream<true, true>(const StreamArgs&, bool, hipStream_t);
-#endif
 
 }  // namespace fp

@@ -25,6 +25,35 @@ void check_2d(const at::Tensor& t, const char* name, at::ScalarType dt) {
   TORCH_CHECK(t.is_cuda(), name, " must be a HIP device tensor");
 }
 
+// Every tensor of a call lives on x's device (the kernels dereference all of
+// them there; a host pointer would fault the GPU).
+void check_same_device(const at::Tensor& x, const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda() && t.device() == x.device(), name, " must be on ", x.device(),
+              ", got ", t.device());
+}
+
+// A weight [N, K] of the call: K columns (the x row length), on x's device.
+void check_weight(const at::Tensor& x, const at::Tensor& w, const char* name) {
+  TORCH_CHECK(w.size(1) == x.size(1), name, " has ", w.size(1), " columns, x has K = ",
+              x.size(1));
+  check_same_device(x, w, name);
+}
+
+// Per-row int8 scales of weight q: contiguous 1-D fp32, one per row, on x's
+// device.
+void check_scale(const at::Tensor& x, const at::Tensor& s, const at::Tensor& q, const char* name) {
+  TORCH_CHECK(s.dim() == 1 && s.scalar_type() == at::kFloat && s.is_contiguous(), name,
+              " must be a contiguous 1-D float32 tensor");
+  TORCH_CHECK(s.size(0) == q.size(0), name, " has ", s.size(0), " rows, q has ", q.size(0));
+  check_same_device(x, s, name);
+}
+
+// Gate and up weights of one call have the same shape.
+void check_pair(const at::Tensor& g, const at::Tensor& u, const char* gn, const char* un) {
+  TORCH_CHECK(g.sizes() == u.sizes(), gn, " ", g.sizes(), " and ", un, " ", u.sizes(),
+              " must have the same shape");
+}
+
 void* cur_stream(const at::Tensor& t) {
   return (void*)c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
@@ -46,6 +75,7 @@ at::Tensor workspace_w8(const at::Tensor& x, int64_t M, int64_t N, int64_t K, bo
 at::Tensor qkv(const at::Tensor& x, const at::Tensor& w, int64_t n_q, int64_t n_k) {
   check_2d(x, "x", at::kBFloat16);
   check_2d(w, "W_qkv", at::kBFloat16);
+  check_weight(x, w, "W_qkv");
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
@@ -61,6 +91,9 @@ at::Tensor gate_up_silu(const at::Tensor& x, const at::Tensor& wg, const at::Ten
   check_2d(x, "x", at::kBFloat16);
   check_2d(wg, "Wg", at::kBFloat16);
   check_2d(wu, "Wu", at::kBFloat16);
+  check_weight(x, wg, "Wg");
+  check_weight(x, wu, "Wu");
+  check_pair(wg, wu, "Wg", "Wu");
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = wg.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
@@ -77,9 +110,8 @@ at::Tensor qkv_w8(const at::Tensor& x, const at::Tensor& q, const at::Tensor& s,
                   int64_t n_k) {
   check_2d(x, "x", at::kBFloat16);
   check_2d(q, "q", at::kChar);
-  TORCH_CHECK(s.dim() == 1 && s.scalar_type() == at::kFloat && s.is_contiguous(),
-              "scale must be a contiguous 1-D float32 tensor");
-  TORCH_CHECK(s.size(0) == q.size(0), "scale has ", s.size(0), " rows, q has ", q.size(0));
+  check_weight(x, q, "q");
+  check_scale(x, s, q, "scale");
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = q.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
@@ -96,10 +128,11 @@ at::Tensor gate_up_silu_w8(const at::Tensor& x, const at::Tensor& qg, const at::
   check_2d(x, "x", at::kBFloat16);
   check_2d(qg, "qg", at::kChar);
   check_2d(qu, "qu", at::kChar);
-  for (const at::Tensor* s : {&sg, &su})
-    TORCH_CHECK(s->dim() == 1 && s->scalar_type() == at::kFloat && s->is_contiguous() &&
-                    s->size(0) == qg.size(0),
-                "scales must be contiguous 1-D float32 tensors with one entry per row");
+  check_weight(x, qg, "qg");
+  check_weight(x, qu, "qu");
+  check_pair(qg, qu, "qg", "qu");
+  check_scale(x, sg, qg, "sg");
+  check_scale(x, su, qu, "su");
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = qg.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
@@ -117,6 +150,7 @@ at::Tensor gate_up_silu_w8(const at::Tensor& x, const at::Tensor& qg, const at::
 at::Tensor linear(const at::Tensor& x, const at::Tensor& w) {
   check_2d(x, "x", at::kBFloat16);
   check_2d(w, "W", at::kBFloat16);
+  check_weight(x, w, "W");
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
@@ -131,9 +165,8 @@ at::Tensor linear(const at::Tensor& x, const at::Tensor& w) {
 at::Tensor linear_w8(const at::Tensor& x, const at::Tensor& q, const at::Tensor& s) {
   check_2d(x, "x", at::kBFloat16);
   check_2d(q, "q", at::kChar);
-  TORCH_CHECK(s.dim() == 1 && s.scalar_type() == at::kFloat && s.is_contiguous(),
-              "scale must be a contiguous 1-D float32 tensor");
-  TORCH_CHECK(s.size(0) == q.size(0), "scale has ", s.size(0), " rows, q has ", q.size(0));
+  check_weight(x, q, "q");
+  check_scale(x, s, q, "scale");
   const c10::DeviceGuard guard(x.device());
   const int64_t M = x.size(0), K = x.size(1), N = q.size(0);
   at::Tensor y = at::empty({M, N}, x.options());
@@ -147,29 +180,29 @@ at::Tensor linear_w8(const at::Tensor& x, const at::Tensor& q, const at::Tensor&
 
 // ---- RMSNorm prologue fused with the projections ----
 
-void check_gamma(const at::Tensor& gamma, int64_t K) {
+void check_gamma(const at::Tensor& x, const at::Tensor& gamma) {
   TORCH_CHECK(gamma.dim() == 1 && gamma.scalar_type() == at::kBFloat16 && gamma.is_contiguous(),
               "norm weight must be a contiguous 1-D bfloat16 tensor");
-  TORCH_CHECK(gamma.size(0) == K, "norm weight has ", gamma.size(0), " elements, x has K = ", K);
-  TORCH_CHECK(gamma.is_cuda(), "norm weight must be a HIP device tensor");
+  TORCH_CHECK(gamma.size(0) == x.size(1), "norm weight has ", gamma.size(0),
+              " elements, x has K = ", x.size(1));
+  check_same_device(x, gamma, "norm weight");
 }
 
-// Workspace for a fused-norm call: what the library asks for, and at least
-// room for the normalised rows (decode-sized calls whose pointers do not fit
-// the one-launch path fall back to it).
+// Workspace for a fused-norm call: what the library asks for (enough for any
+// pointers and strides of the shape).
 at::Tensor norm_workspace(const at::Tensor& x, int64_t M, int64_t N, int64_t K, bool gate_up,
                           bool int8) {
-  int64_t bytes = fp_rmsnorm_workspace_bytes(M, N, K, gate_up ? 1 : 0, int8 ? 1 : 0);
-  const int64_t rows = (M * K * 2 + 255) / 256 * 256;
-  return at::empty({bytes > rows ? bytes : rows}, x.options().dtype(at::kByte));
+  const int64_t bytes = fp_rmsnorm_workspace_bytes(M, N, K, gate_up ? 1 : 0, int8 ? 1 : 0);
+  return at::empty({bytes}, x.options().dtype(at::kByte));
 }
 
 at::Tensor rmsnorm_qkv(const at::Tensor& x, const at::Tensor& gamma, double eps,
                        const at::Tensor& w, int64_t n_q, int64_t n_k) {
   check_2d(x, "x", at::kBFloat16);
   check_2d(w, "W_qkv", at::kBFloat16);
+  check_weight(x, w, "W_qkv");
   const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
-  check_gamma(gamma, K);
+  check_gamma(x, gamma);
   const c10::DeviceGuard guard(x.device());
   at::Tensor y = at::empty({M, N}, x.options());
   at::Tensor ws = norm_workspace(x, M, N, K, false, false);
@@ -185,8 +218,11 @@ at::Tensor rmsnorm_gate_up_silu(const at::Tensor& x, const at::Tensor& gamma, do
   check_2d(x, "x", at::kBFloat16);
   check_2d(wg, "Wg", at::kBFloat16);
   check_2d(wu, "Wu", at::kBFloat16);
+  check_weight(x, wg, "Wg");
+  check_weight(x, wu, "Wu");
+  check_pair(wg, wu, "Wg", "Wu");
   const int64_t M = x.size(0), K = x.size(1), N = wg.size(0);
-  check_gamma(gamma, K);
+  check_gamma(x, gamma);
   const c10::DeviceGuard guard(x.device());
   at::Tensor y = at::empty({M, N}, x.options());
   at::Tensor ws = norm_workspace(x, M, N, K, true, false);
@@ -199,19 +235,14 @@ at::Tensor rmsnorm_gate_up_silu(const at::Tensor& x, const at::Tensor& gamma, do
   return y;
 }
 
-void check_scale(const at::Tensor& s, const at::Tensor& q, const char* name) {
-  TORCH_CHECK(s.dim() == 1 && s.scalar_type() == at::kFloat && s.is_contiguous(), name,
-              " must be a contiguous 1-D float32 tensor");
-  TORCH_CHECK(s.size(0) == q.size(0), name, " has ", s.size(0), " rows, q has ", q.size(0));
-}
-
 at::Tensor rmsnorm_qkv_w8(const at::Tensor& x, const at::Tensor& gamma, double eps,
                           const at::Tensor& q, const at::Tensor& s, int64_t n_q, int64_t n_k) {
   check_2d(x, "x", at::kBFloat16);
   check_2d(q, "q", at::kChar);
-  check_scale(s, q, "scale");
+  check_weight(x, q, "q");
+  check_scale(x, s, q, "scale");
   const int64_t M = x.size(0), K = x.size(1), N = q.size(0);
-  check_gamma(gamma, K);
+  check_gamma(x, gamma);
   const c10::DeviceGuard guard(x.device());
   at::Tensor y = at::empty({M, N}, x.options());
   at::Tensor ws = norm_workspace(x, M, N, K, false, true);
@@ -229,10 +260,13 @@ at::Tensor rmsnorm_gate_up_silu_w8(const at::Tensor& x, const at::Tensor& gamma,
   check_2d(x, "x", at::kBFloat16);
   check_2d(qg, "qg", at::kChar);
   check_2d(qu, "qu", at::kChar);
-  check_scale(sg, qg, "sg");
-  check_scale(su, qu, "su");
+  check_weight(x, qg, "qg");
+  check_weight(x, qu, "qu");
+  check_pair(qg, qu, "qg", "qu");
+  check_scale(x, sg, qg, "sg");
+  check_scale(x, su, qu, "su");
   const int64_t M = x.size(0), K = x.size(1), N = qg.size(0);
-  check_gamma(gamma, K);
+  check_gamma(x, gamma);
   const c10::DeviceGuard guard(x.device());
   at::Tensor y = at::empty({M, N}, x.options());
   at::Tensor ws = norm_workspace(x, M, N, K, true, true);

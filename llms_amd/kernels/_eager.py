@@ -88,17 +88,25 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, start_pos) -> torc
     The core runs in fp32 on contiguous operands and casts back to q.dtype:
     the result then does not depend on which SDPA backend torch would pick,
     and no bf16 batched product sees a transposed operand.
+
+    With a device-tensor ``start_pos`` the cache slots past the last query
+    position are never attended, and they may hold anything (a cache
+    allocated with ``torch.empty``, as the reference's ``KVCache.alloc`` does):
+    their scores are masked to -inf and their values are zeroed before
+    ``p @ v``, so NaN or Inf there cannot reach the output (0 * NaN is NaN).
     """
     T, S = q.shape[2], k.shape[2]
+    vf = v.float()
     scores = torch.matmul(q.float().contiguous(), k.float().transpose(-2, -1).contiguous())
     scores = scores * (q.shape[-1] ** -0.5)
     if torch.is_tensor(start_pos):
         q_pos = (start_pos + torch.arange(T, device=q.device))[:, None]
         k_pos = torch.arange(S, device=q.device)[None, :]
         scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
+        vf = vf.masked_fill((k_pos > q_pos[-1]).reshape(S, 1), 0.0)
     elif T > 1:
         q_pos = torch.arange(start_pos, start_pos + T, device=q.device)[:, None]
         k_pos = torch.arange(S, device=q.device)[None, :]
         scores = scores.masked_fill(k_pos > q_pos, float("-inf"))
     p = torch.softmax(scores, dim=-1)
-    return torch.matmul(p, v.float().contiguous()).to(q.dtype)
+    return torch.matmul(p, vf.contiguous()).to(q.dtype)

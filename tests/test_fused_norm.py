@@ -70,16 +70,19 @@ def check_norm_gate_up(M, K, N, seed=0, std=3.0, eps=EPS):
 
 
 def test_workspace_bytes_and_errors():
-    """Decode-sized calls need no workspace (one launch); others need the
-    normalised rows (plus split partials); argument errors come back before
-    any launch."""
+    """The workspace query always leaves room for the normalised rows:
+    decode-sized calls usually run as one launch and leave it unused, but
+    fall back to the two-launch path when a pointer or stride is not 16-byte
+    aligned; larger calls add split partials. Argument errors come back
+    before any launch."""
     from llms_amd import _lib
 
     lib = _lib.capi()
     wb = lib.fp_rmsnorm_workspace_bytes
-    assert wb(1, 6144, 2560, 0, 0) == 0 and wb(2, 9728, 2560, 1, 0) == 0
-    assert wb(4, 9728, 2560, 1, 1) == 0            # int8 rows kernel to 4 rows
-    assert wb(3, 6144, 2560, 0, 0) == (3 * 2560 * 2 + 255) // 256 * 256  # bf16 from 3 rows
+    rows = lambda M, K: (M * K * 2 + 255) // 256 * 256  # noqa: E731
+    assert wb(1, 6144, 2560, 0, 0) == rows(1, 2560) and wb(2, 9728, 2560, 1, 0) == rows(2, 2560)
+    assert wb(4, 9728, 2560, 1, 1) == rows(4, 2560)   # int8 rows kernel to 4 rows
+    assert wb(3, 6144, 2560, 0, 0) == rows(3, 2560)   # bf16 from 3 rows
     assert wb(1, 6144, 2541, 0, 0) == (2541 * 2 + 255) // 256 * 256  # K % 8 != 0
     assert wb(512, 2560, 9728, 0, 0) > 512 * 9728 * 2  # rows + split partials
     P = ctypes.c_void_p(16)
@@ -207,13 +210,28 @@ def test_norm_deterministic_and_raw_abi(M):
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     need = lib.fp_rmsnorm_workspace_bytes(M, N, K, 0, 0)
+    assert need >= (M * K * 2 + 255) // 256 * 256
     st = lib.fp_rmsnorm_qkv_bf16(P(x), K, P(g), EPS, P(w), K, P(y), N, M, n_q, n_k, K, None, 0, stream)
-    if need:
+    if M > 2:  # past the one-launch decode path: the normalised rows need room
         assert st == 6
         torch.cuda.synchronize()
         assert torch.all(y == 7.0)
     else:
         assert st == 0
+    if M <= 2:
+        # an odd row stride keeps x off the one-launch path: the queried
+        # workspace is enough for the two-launch path
+        xs = torch.zeros(M, K + 1, dtype=torch.bfloat16, device=DEV)
+        xs[:, :K] = x
+        ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+        y2 = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=DEV)
+        assert lib.fp_rmsnorm_qkv_bf16(P(xs), K + 1, P(g), EPS, P(w), K, P(y2), N, M, n_q, n_k, K,
+                                       None, 0, stream) == 6
+        assert lib.fp_rmsnorm_qkv_bf16(P(xs), K + 1, P(g), EPS, P(w), K, P(y2), N, M, n_q, n_k, K,
+                                       P(ws), need, stream) == 0
+        torch.cuda.synchronize()
+        _check(y2.cpu(), ref.ref_rmsnorm_qkv_full(bits(x), bits(g), EPS, bits(w), n_q, n_k),
+               f"norm+qkv strided x M={M}")
     ws = torch.empty(max(need, 16), dtype=torch.uint8, device=DEV)
     assert lib.fp_rmsnorm_qkv_bf16(P(x), K, P(g), EPS, P(w), K, P(y), N, M, n_q, n_k, K, P(ws),
                                    need, stream) == 0

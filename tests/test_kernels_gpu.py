@@ -512,14 +512,23 @@ def test_qwen3_8b_sweep(M):
     check_ffn(50 + M, M, K, I, label=f"8B gate-up M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 16, 256])
+@pytest.mark.parametrize("M", [1, 4, 16, 64, 256, 4096])
 def test_qwen3_8b_int8(M):
-    K, _, _, I = QWEN3_8B
+    """BASELINE's Qwen3-8B sweep with int8 weights, both projections, against
+    the dequantise-then-matmul oracle (a seeded subset of rows at large M)."""
+    K, n_q, n_k, I = QWEN3_8B
+    kern = _kernels()
+    rows = _rows(M)
+    x, w = qkv_inputs(80 + M, M, K, n_q, n_k)
+    q, s = _quant(w)
+    y = torch.cat(kern.fused_qkv_w8(x.to(DEV), q, s, n_q=n_q, n_k=n_k), dim=-1).cpu()
+    out = ref.ref_qkv_w8_full(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy(), n_q, n_k)
+    _check(y[rows], out, f"8B int8 qkv M={M}")
+    del q, s, y
     x, wg, wu = ffn_inputs(60 + M, M, K, I)
     qg, sg = _quant(wg)
     qu, su = _quant(wu)
-    y = _kernels().fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
-    rows = _rows(M)
+    y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
     out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
                                        qu.cpu().numpy(), su.cpu().numpy())
     _check(y[rows], out, f"8B int8 gate-up M={M}")
