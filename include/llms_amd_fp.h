@@ -17,9 +17,10 @@
  *     stride in ELEMENTS. Weights use the nn.Linear layout [N, K].
  *   - stream is a hipStream_t (NULL = the legacy default stream). Every call
  *     is asynchronous on that stream; nothing is allocated, freed or
- *     synchronised; no global state is written; calls are reentrant. The
- *     *_ws variants also write the caller's workspace, which must not be
- *     used by work that can overlap the call.
+ *     synchronised; calls are reentrant. The *_ws variants also write the
+ *     caller's workspace, which must not be used by work that can overlap
+ *     the call. The only global state is the per-device address of the
+ *     static scratch of fp_rmsnorm_qkv_bf16_noalloc, written once per device.
  *   - Return 0 (FP_OK) on success, a nonzero fp_status otherwise; argument
  *     errors are detected before anything is launched.
  *   - Results are deterministic: the same inputs give bit-identical outputs
@@ -51,8 +52,10 @@ typedef enum fp_status {
   FP_ERR_STRIDE = 3,     /* a row stride is smaller than the row length */
   FP_ERR_LAUNCH = 4,     /* the HIP launch reported an error */
   FP_ERR_DEVICE = 5,     /* no usable gfx950 device for the current context */
-  FP_ERR_WORKSPACE = 6   /* workspace missing or too small where required, not 16-byte
+  FP_ERR_WORKSPACE = 6,  /* workspace missing or too small where required, not 16-byte
                             aligned, or a negative size */
+  FP_ERR_SCRATCH = 7     /* the call needs more than the library's static scratch
+                            (FP_SCRATCH_BYTES); use the workspace entry point */
 } fp_status;
 
 /* Human-readable text for an fp_status value (static storage). */
@@ -253,6 +256,28 @@ int fp_rmsnorm_gate_up_silu_w8(const void* x, int64_t ldx, const void* gamma, fl
                                int64_t M, int64_t N, int64_t K,
                                void* workspace, int64_t workspace_bytes,
                                void* stream);
+
+/*
+ * Allocation-free variant of fp_rmsnorm_qkv_bf16 (no reference counterpart:
+ * for callers that cannot allocate device memory — code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). Same
+ * arguments, contract and results as fp_rmsnorm_qkv_bf16, bit for bit, but
+ * the workspace is the library's own static device array of FP_SCRATCH_BYTES
+ * (one per GPU, held until the process ends; its address is looked up once
+ * per device on the first call there). Calls whose
+ * fp_rmsnorm_workspace_bytes(M, n_q + 2*n_k, K, 0, 0) exceeds FP_SCRATCH_BYTES
+ * return FP_ERR_SCRATCH before anything is launched. Every call on a GPU
+ * overwrites that GPU's scratch: calls that can overlap on one GPU (streams
+ * without ordering between them) race and must be serialised by the caller.
+ * Nothing is allocated or freed.
+ */
+#define FP_SCRATCH_BYTES (32u << 20)
+
+int fp_rmsnorm_qkv_bf16_noalloc(const void* x, int64_t ldx, const void* gamma, float eps,
+                                const void* w, int64_t ldw,
+                                void* y, int64_t ldy,
+                                int64_t M, int64_t n_q, int64_t n_k, int64_t K,
+                                void* stream);
 
 /*
  * Per-output-channel symmetric int8 quantisation on the device (the packing

@@ -55,6 +55,7 @@ CAPI_SIGNATURES: dict[str, list] = {
     "fp_rmsnorm_qkv_w8": [_P, _I64, _P, _F, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "fp_rmsnorm_gate_up_silu_w8": [_P, _I64, _P, _F, _P, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64,
                                    _I64, _P, _I64, _P],
+    "fp_rmsnorm_qkv_bf16_noalloc": [_P, _I64, _P, _F, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P],
 }
 
 FP_STATUS = {
@@ -65,7 +66,12 @@ FP_STATUS = {
     4: "FP_ERR_LAUNCH",
     5: "FP_ERR_DEVICE",
     6: "FP_ERR_WORKSPACE",
+    7: "FP_ERR_SCRATCH",
 }
+
+# FP_SCRATCH_BYTES of include/llms_amd_fp.h: the static scratch of
+# fp_rmsnorm_qkv_bf16_noalloc, per GPU.
+FP_SCRATCH_BYTES = 32 << 20
 
 
 def _missing(path: Path) -> NativeLibraryMissing:

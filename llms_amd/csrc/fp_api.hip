@@ -197,6 +197,19 @@ int check_common(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy) {
 }
 
 }  // namespace
+
+int rmsnorm_qkv_args(const void* x, int64_t ldx, const void* gamma, float eps, const void* w,
+                     int64_t ldw, const void* y, int64_t ldy, int64_t M, int64_t n_q, int64_t n_k,
+                     int64_t K) {
+  if (n_q < 1 || n_k < 0) return FP_ERR_SHAPE;
+  int st = check_common(M, n_q + 2 * n_k, K, ldx, ldy);
+  if (st) return st;
+  if (ldw < K) return FP_ERR_STRIDE;
+  if ((st = check_norm(eps, nullptr, 0))) return st;
+  if (M > 0 && (!x || !gamma || !w || !y)) return FP_ERR_NULL;
+  return FP_OK;
+}
+
 }  // namespace fp
 
 using fp::StreamArgs;
@@ -212,6 +225,7 @@ const char* fp_status_string(int status) {
     case FP_ERR_LAUNCH: return "HIP kernel launch failed";
     case FP_ERR_DEVICE: return "no gfx950 code object for the current device";
     case FP_ERR_WORKSPACE: return "workspace missing, too small or not 16-byte aligned, or a negative workspace size";
+    case FP_ERR_SCRATCH: return "the call needs more than the library's static scratch (FP_SCRATCH_BYTES); use the workspace entry point";
     default: return "unknown fp_status";
   }
 }
@@ -364,14 +378,11 @@ int64_t fp_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up,
 int fp_rmsnorm_qkv_bf16(const void* x, int64_t ldx, const void* gamma, float eps, const void* w,
                         int64_t ldw, void* y, int64_t ldy, int64_t M, int64_t n_q, int64_t n_k,
                         int64_t K, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (n_q < 1 || n_k < 0) return FP_ERR_SHAPE;
-  const int64_t N = n_q + 2 * n_k;
-  int st = fp::check_common(M, N, K, ldx, ldy);
+  int st = fp::rmsnorm_qkv_args(x, ldx, gamma, eps, w, ldw, y, ldy, M, n_q, n_k, K);
   if (st) return st;
-  if (ldw < K) return FP_ERR_STRIDE;
   if ((st = fp::check_norm(eps, workspace, workspace_bytes))) return st;
   if (M == 0) return FP_OK;
-  if (!x || !gamma || !w || !y) return FP_ERR_NULL;
+  const int64_t N = n_q + 2 * n_k;
   StreamArgs a{(const uint16_t*)x, ldx, w, ldw, nullptr, 0, nullptr, nullptr, (uint16_t*)y, ldy,
                M, N, K, nullptr, 0, (const uint16_t*)gamma, eps};
   const bool xal = K % 8 == 0 && ldx % 8 == 0 && fp::al16(x);

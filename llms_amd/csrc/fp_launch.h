@@ -142,4 +142,10 @@ int launch_quantize_w8(const uint16_t* w, int64_t ldw, int8_t* q, int64_t ldq,
 
 constexpr int64_t kStreamMaxM = 64;
 
+// Argument checks of fp_rmsnorm_qkv_bf16 other than its workspace (the
+// fp_status of the first problem, FP_OK if none); nothing touches a device.
+int rmsnorm_qkv_args(const void* x, int64_t ldx, const void* gamma, float eps, const void* w,
+                     int64_t ldw, const void* y, int64_t ldy, int64_t M, int64_t n_q, int64_t n_k,
+                     int64_t K);
+
 }  // namespace fp
