@@ -105,6 +105,25 @@ __device__ __forceinline__ uint32_t gate_up_silu_bits(float acc_g, float acc_u) 
   return f32_to_bf16_bits(s * u);
 }
 
+// Two outputs of the same epilogue, packed as two bf16 (lo: (g0, u0), hi:
+// (g1, u1)); bit-identical to gate_up_silu_bits on each. The conversions of
+// the two outputs share each v_cvt_pk_bf16_f32 (one for g and u of an
+// output, one for both silu values, one for both products), and NaN
+// canonicalisation runs only in waves that hold a NaN.
+__device__ __forceinline__ uint32_t gate_up_silu_pair(float g0, float u0, float g1, float u1) {
+  const uint32_t a = cvt_bf16x2(g0, u0), b = cvt_bf16x2(g1, u1);
+  const float ga = __uint_as_float(a << 16), ua = __uint_as_float(a & 0xffff0000u);
+  const float gb = __uint_as_float(b << 16), ub = __uint_as_float(b & 0xffff0000u);
+  const uint32_t s = cvt_bf16x2(__fdividef(ga, 1.0f + __expf(-ga)), __fdividef(gb, 1.0f + __expf(-gb)));
+  const float ya = __uint_as_float(s << 16) * ua, yb = __uint_as_float(s & 0xffff0000u) * ub;
+  uint32_t y = cvt_bf16x2(ya, yb);
+  if (__builtin_expect((ya != ya) | (yb != yb), 0)) {
+    if (ya != ya) y = (y & 0xffff0000u) | 0x7fc0u;
+    if (yb != yb) y = (y & 0xffffu) | 0x7fc00000u;
+  }
+  return y;
+}
+
 // ---- memory ---------------------------------------------------------------
 
 // 16-byte global load (global_load_dwordx4). p must be 16-byte aligned.
