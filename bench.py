@@ -427,6 +427,56 @@ def ship_gate_run(torch, kern, warmup: int = 50, iters: int = 200) -> dict:
     return out
 
 
+def read_ceiling_run(torch, kern, reps: int) -> dict:
+    """The read-only ceiling of the decode launches: libllms_amd_probe.so's
+    read kernel (the row-streaming kernels' memory pattern, no arithmetic)
+    over the same 36 cycled Qwen3-4B weight buffers, gate-up-shaped (Wg and Wu
+    rows read as pairs, 99.6 MB) and QKV-shaped (31.5 MB), timed like the
+    projections (graph replay, HIP events on the replay stream); the fused
+    kernels on the same buffers alongside. An empty kernel gives the launch
+    floor."""
+    import ctypes
+
+    from llms_amd import build as B
+
+    if not B.PROBE_SO.exists():
+        raise RuntimeError(f"{B.PROBE_SO} is not built (python -m llms_amd.build)")
+    probe = ctypes.CDLL(str(B.PROBE_SO))
+    probe.fp_probe_read_rows.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    probe.fp_probe_read_rows.restype = ctypes.c_int
+    K, n_q, n_k, inter = SHAPES["qwen3-4b"]
+    n_qkv = n_q + 2 * n_k
+    L = 36
+    stack = Stack(torch, SHAPES["qwen3-4b"], L, M=1)
+    sink = torch.empty(inter, dtype=torch.int32, device="cuda")
+    row_kb = K * 2 // 1024
+
+    def rd(p0, p1, rows):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        rc = probe.fp_probe_read_rows(p0.data_ptr(), p1.data_ptr() if p1 is not None else None,
+                                      rows, row_kb, sink.data_ptr(), st)
+        assert rc == 0, rc
+
+    out = {"mode": "read_ceiling", "weight_sets": L, "shape": "qwen3-4b"}
+    t = kernel_seconds(torch, [lambda l=l: rd(stack.wg[l], stack.wu[l], inter) for l in range(L)], reps)
+    out["read_gate_up_us"] = round(t * 1e6, 3)
+    out["read_gate_up_gbs"] = round(2 * inter * K * 2 / t / 1e9, 1)
+    t = kernel_seconds(torch, [lambda l=l: rd(stack.wqkv[l], None, n_qkv) for l in range(L)], reps)
+    out["read_qkv_us"] = round(t * 1e6, 3)
+    out["read_qkv_gbs"] = round(n_qkv * K * 2 / t / 1e9, 1)
+    t = kernel_seconds(torch, [lambda l=l: kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l])
+                               for l in range(L)], reps)
+    out["fused_gate_up_us"] = round(t * 1e6, 3)
+    t = kernel_seconds(torch, [lambda l=l: kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k)
+                               for l in range(L)], reps)
+    out["fused_qkv_us"] = round(t * 1e6, 3)
+    # launch floor: the probe on one row (one workgroup, 8 KB)
+    t = kernel_seconds(torch, [lambda l=l: rd(stack.wqkv[l], None, 1) for l in range(L)], reps)
+    out["one_row_launch_us"] = round(t * 1e6, 3)
+    return out
+
+
 # Every configuration BASELINE.json lists: (model, M, int8).
 CONFIGS = ([("qwen3-0.6b", 1, False)]
            + [("qwen3-4b", m, False) for m in (1, 3, 4, 8, 512, 2048, 8192)]
@@ -516,6 +566,9 @@ def main() -> int:
     ap.add_argument("--ship-gate", action="store_true",
                     help="the reference's microbench ship gate (fused <= eager at M = 1, 5, 8 "
                          "on Qwen3-4B QKV and gate-up); prints one JSON line")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="time the read-only probe (the decode kernels' memory pattern, no "
+                         "arithmetic) on the decode weight buffers; prints one JSON line")
     ap.add_argument("--linear", metavar="M,N,K",
                     help="time only the plain projection (down / o) of this shape over "
                          "cycled weight sets and print one JSON line (profiling aid)")
@@ -549,6 +602,9 @@ def main() -> int:
         return 0
     if args.configs:
         configs_run(torch, kern, args.steps)
+        return 0
+    if args.read_ceiling:
+        print(json.dumps(read_ceiling_run(torch, kern, args.steps)), flush=True)
         return 0
     if args.ship_gate:
         print(json.dumps(ship_gate_run(torch, kern)), flush=True)

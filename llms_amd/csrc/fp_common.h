@@ -131,6 +131,14 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// 16-byte global load with the non-temporal hint (global_load_dwordx4 ... nt):
+// for weight streams that are read once per call. Measured on MI355X on a
+// read-only kernel with the decode kernels' pattern over 36 cycled weight
+// sets (99.6 MB per launch): 17.12 -> 15.63 us.
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
 // Eight bf16 starting at element k of a row of length K, zero beyond K.
 // ALIGNED: the row base is 16-byte aligned and K % 8 == 0, so a chunk of eight
 // starting at a multiple of 8 lies wholly inside or wholly outside the row.

@@ -84,12 +84,18 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
         xg[u] = load_bf16x8<true>(a.x, k, K);
         if constexpr (W8) xg1[u] = load_bf16x8<true>(a.x, k + 8, K);
       }
-      if constexpr (W8) {
-        wg[u] = load_i8x16<true>((const int8_t*)a.w0 + row * a.ldw0, k, K);
-        if constexpr (GATEUP) wu[u] = load_i8x16<true>((const int8_t*)a.w1 + row * a.ldw1, k, K);
+      // weights: read once per call, non-temporal; zero past the row's end
+      if (k < K) {
+        if constexpr (W8) {
+          wg[u] = ld16_nt((const int8_t*)a.w0 + row * a.ldw0 + k);
+          if constexpr (GATEUP) wu[u] = ld16_nt((const int8_t*)a.w1 + row * a.ldw1 + k);
+        } else {
+          wg[u] = ld16_nt((const uint16_t*)a.w0 + row * a.ldw0 + k);
+          if constexpr (GATEUP) wu[u] = ld16_nt((const uint16_t*)a.w1 + row * a.ldw1 + k);
+        }
       } else {
-        wg[u] = load_bf16x8<true>((const uint16_t*)a.w0 + row * a.ldw0, k, K);
-        if constexpr (GATEUP) wu[u] = load_bf16x8<true>((const uint16_t*)a.w1 + row * a.ldw1, k, K);
+        wg[u] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (GATEUP) wu[u] = u32x4{0u, 0u, 0u, 0u};
       }
       if (++ij == J) { ij = 0; ++ir; }
     }
