@@ -180,6 +180,19 @@ __device__ __forceinline__ u32x4 load_i8x16(const int8_t* row, int64_t k, int64_
   }
 }
 
+// Weight-stream forms of the two loads above: the aligned path uses the
+// non-temporal hint (weights are read once per decode-regime call).
+template <bool ALIGNED>
+__device__ __forceinline__ u32x4 load_w_bf16x8(const uint16_t* row, int64_t k, int64_t K) {
+  if constexpr (ALIGNED) return k < K ? ld16_nt(row + k) : u32x4{0u, 0u, 0u, 0u};
+  return load_bf16x8<false>(row, k, K);
+}
+template <bool ALIGNED>
+__device__ __forceinline__ u32x4 load_w_i8x16(const int8_t* row, int64_t k, int64_t K) {
+  if constexpr (ALIGNED) return k < K ? ld16_nt(row + k) : u32x4{0u, 0u, 0u, 0u};
+  return load_i8x16<false>(row, k, K);
+}
+
 // ---- int8 -> bf16 dequantisation ------------------------------------------
 //
 // w = bf16_rne(fp32(q * s)), bit-identical to (q.float() * s).to(bfloat16):

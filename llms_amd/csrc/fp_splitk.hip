@@ -36,13 +36,16 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & (kCPR - 1); }
 __device__ __forceinline__ int swz8(int r) { return (r >> 2) & 3; }
 
 // buffer_load_dwordx4 ... lds: 16 bytes per lane from base + voff + soff into
-// LDS at dst + 16 * lane; bytes at or past `nbytes` read as zero.
+// LDS at dst + 16 * lane; bytes at or past `nbytes` read as zero. NT: the
+// non-temporal hint (cache-policy bit 1), for the weight stream, which a
+// call reads once.
+template <bool NT = false>
 __device__ __forceinline__ void load_lds16(const void* base, int nbytes, lds_ptr_t dst,
                                            uint32_t voff, uint32_t soff) {
   constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, kRsrcFlags), dst, 16,
-      voff, soff, 0, 0);
+      voff, soff, 0, NT ? 2 : 0);
 }
 
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= v only.
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
     for (int q = 0; q < IW; ++q) {
       // instruction q holds 16-row groups of one matrix (uniform per instruction)
       const bool up = wrow_up(q * WRPI);
-      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0, (lds_ptr_t)(t + q * 1024), woff[q],
+      load_lds16<true>(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0, (lds_ptr_t)(t + q * 1024), woff[q],
                  (uint32_t)(k0 * WB));
     }
 #pragma unroll

@@ -132,13 +132,13 @@ __global__ __launch_bounds__(NW * kWave) void stream_kernel(StreamArgs a) {
     const int64_t kw = kb * KB + chunk * CK;
     const u32x4 z{0, 0, 0, 0};
     if constexpr (W8) {
-      f.a0 = (live && row_ok) ? load_i8x16<ALIGNED>((const int8_t*)w0row, kw, K) : z;
+      f.a0 = (live && row_ok) ? load_w_i8x16<ALIGNED>((const int8_t*)w0row, kw, K) : z;
       if constexpr (GATEUP)
-        f.a1 = (live && row_ok) ? load_i8x16<ALIGNED>((const int8_t*)w1row, kw, K) : z;
+        f.a1 = (live && row_ok) ? load_w_i8x16<ALIGNED>((const int8_t*)w1row, kw, K) : z;
     } else {
-      f.a0 = (live && row_ok) ? load_bf16x8<ALIGNED>((const uint16_t*)w0row, kw, K) : z;
+      f.a0 = (live && row_ok) ? load_w_bf16x8<ALIGNED>((const uint16_t*)w0row, kw, K) : z;
       if constexpr (GATEUP)
-        f.a1 = (live && row_ok) ? load_bf16x8<ALIGNED>((const uint16_t*)w1row, kw, K) : z;
+        f.a1 = (live && row_ok) ? load_w_bf16x8<ALIGNED>((const uint16_t*)w1row, kw, K) : z;
     }
     if constexpr (!XL) {
 #pragma unroll
