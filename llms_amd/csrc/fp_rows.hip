@@ -331,11 +331,18 @@ template bool rows_supported<true>(const StreamArgs&, bool);
 
 // Measured on MI355X (Qwen3-4B and -8B, 24-36 cycled weight sets): the whole
 // row in flight (K = 2560: 5 bf16 or 3 int8 chunks); bf16 one row (pair) per
-// wave, 8 waves per workgroup; int8 gate-up two row pairs per wave and 4
-// waves up to 2 x rows, one and 8 waves for 3..4; x rows rounded up to 1, 2, 4.
+// wave, 8 waves per workgroup; int8 with one x row read from L2 (K <= 2560,
+// no fused norm): one row (pair) per wave, 4 waves per workgroup (with the
+// non-temporal weight stream: 4B gate-up 12.51 -> 11.75 us against two row
+// pairs per wave, QKV 5.85 -> 5.43 us against 8 waves; with x staged in LDS,
+// 8B K = 4096, the 4-wave workgroups are 14% slower); otherwise int8 gate-up
+// two row pairs per wave and 4 waves up to 2 x rows, one and 8 waves for
+// 3..4; x rows rounded up to 1, 2, 4.
 template <int MM, bool GATEUP, bool W8>
 int launch_rows_m(const StreamArgs& a, hipStream_t s) {
   if constexpr (W8) {
+    if constexpr (MM == 1)
+      if (!a.gamma && a.K <= 2560) return launch_rows_cfg<4, 1, 3, 1, GATEUP, true>(a, s);
     if constexpr (GATEUP && MM <= 2) return launch_rows_cfg<4, 2, 3, MM, true, true>(a, s);
     if constexpr (GATEUP) return launch_rows_cfg<8, 1, 3, MM, true, true>(a, s);
     return launch_rows_cfg<8, 1, 3, MM, false, true>(a, s);
