@@ -234,9 +234,9 @@ def cpu_baseline(torch, stacks: dict, reps: int) -> dict:
 
 def counters_run(torch, kern, shape, layers: int, Mp: int = 2048) -> dict:
     """A short fixed sequence for `rocprofv3 --pmc` runs: a plain device copy
-    of known size (calibrates FETCH_SIZE / WRITE_SIZE), then the decode (M=1)
-    and prefill (M=Mp, default 2048) fused kernels over `layers` cycled weight
-    sets."""
+    of known size (calibrates FETCH_SIZE / WRITE_SIZE), then three passes of
+    the decode (M=1) fused kernels over `layers` cycled weight sets and three
+    of the prefill (M=Mp, default 2048) kernels over 4 of them."""
     K, n_q, n_k, inter = shape
     n_qkv = n_q + 2 * n_k
     copy_bytes = 256 << 20
@@ -247,25 +247,27 @@ def counters_run(torch, kern, shape, layers: int, Mp: int = 2048) -> dict:
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    run_step(stack, kern)
+    for _ in range(3):
+        run_step(stack, kern)
     torch.cuda.synchronize()
     stack.set_m(torch, Mp)
-    for l in range(min(4, layers)):
-        kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k)
-        kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l])
+    for _ in range(3):
+        for l in range(min(4, layers)):
+            kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k)
+            kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l])
     torch.cuda.synchronize()
     return {
         "mode": "counters",
         "copy": {"kernel": "bfloat16_copy_kernel", "read_bytes": copy_bytes,
                  "write_bytes": copy_bytes, "launches": 3},
         "gate_up_m1": {"read_bytes": 2 * K * 2 * inter + 2 * K, "write_bytes": 2 * inter,
-                       "launches": layers},
+                       "launches": 3 * layers},
         "qkv_m1": {"read_bytes": 2 * K * n_qkv + 2 * K, "write_bytes": 2 * n_qkv,
-                   "launches": layers},
+                   "launches": 3 * layers},
         f"gate_up_m{Mp}": {"read_bytes": 2 * K * 2 * inter + 2 * Mp * K,
-                           "write_bytes": 2 * Mp * inter, "launches": min(4, layers)},
+                           "write_bytes": 2 * Mp * inter, "launches": 3 * min(4, layers)},
         f"qkv_m{Mp}": {"read_bytes": 2 * K * n_qkv + 2 * Mp * K,
-                       "write_bytes": 2 * Mp * n_qkv, "launches": min(4, layers)},
+                       "write_bytes": 2 * Mp * n_qkv, "launches": 3 * min(4, layers)},
     }
 
 
@@ -477,6 +479,64 @@ def read_ceiling_run(torch, kern, reps: int) -> dict:
     return out
 
 
+# The kernel families profiled under profiles/ besides the default bench's
+# decode and prefill grids: (label, model, M, int8, which projections).
+PROFILE_SET = [
+    ("int8 decode", "qwen3-4b", 1, True, "both"),
+    ("int8 verify", "qwen3-4b", 4, True, "both"),
+    ("int8 prefill", "qwen3-4b", 2048, True, "both"),
+    ("bf16 verify M=3", "qwen3-4b", 3, False, "both"),
+    ("bf16 verify M=8", "qwen3-4b", 8, False, "both"),
+    ("split-K tiles M=64", "qwen3-8b", 64, False, "both"),
+    ("split-K tiles M=256", "qwen3-8b", 256, False, "both"),
+    ("prefill M=8192", "qwen3-4b", 8192, False, "both"),
+]
+
+
+def profile_set_run(torch, kern, reps: int) -> dict:
+    """A fixed sequence for rocprofv3 runs (kernel trace, --pmc passes): each
+    PROFILE_SET entry over its own cycled weight sets (36 for decode-sized
+    calls, else enough to pass the Infinity Cache), replayed in a HIP graph
+    `reps` times after a short warm-up; one JSON line per entry with the
+    measured per-launch times."""
+    out = {"mode": "profile_set", "entries": []}
+    for label, model, M, int8, _ in PROFILE_SET:
+        K, n_q, n_k, inter = SHAPES[model]
+        n = n_q + 2 * n_k
+        wbytes = (1 if int8 else 2) * K * (n + 2 * inter)
+        sets = 36 if M <= 64 else max(4, min(36, (1200 << 20) // wbytes))
+        g = torch.Generator(device="cuda")
+        g.manual_seed(0)
+        x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+
+        def w(rows):
+            return (torch.randn(rows, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+
+        ws = []
+        for _ in range(sets):
+            t = (w(n), w(inter), w(inter))
+            ws.append(tuple(kern.quantize_w8_per_row(v) for v in t) if int8 else t)
+        if int8:
+            qk = [lambda t=t: kern.fused_qkv_w8(x, t[0][0], t[0][1], n_q=n_q, n_k=n_k) for t in ws]
+            gu = [lambda t=t: kern.fused_gate_up_silu_w8(x, t[1][0], t[1][1], t[2][0], t[2][1])
+                  for t in ws]
+        else:
+            qk = [lambda t=t: kern.triton_fused_qkv(x, t[0], n_q=n_q, n_k=n_k) for t in ws]
+            gu = [lambda t=t: kern.triton_fused_gate_up_silu(x, t[1], t[2]) for t in ws]
+        ent = {"label": label, "model": model, "M": M, "weights": "int8" if int8 else "bf16",
+               "weight_sets": sets}
+        for name, launches in (("qkv", qk), ("gate_up", gu)):
+            graph = capture(torch, lambda: [fn() for fn in launches])
+            sec = time_graph(torch, graph, reps, 2) / len(launches)
+            del graph
+            ent[f"{name}_us"] = round(sec * 1e6, 2)
+        print(json.dumps(ent), flush=True)
+        out["entries"].append(ent)
+        del ws, qk, gu
+        torch.cuda.empty_cache()
+    return out
+
+
 # Every configuration BASELINE.json lists: (model, M, int8).
 CONFIGS = ([("qwen3-0.6b", 1, False)]
            + [("qwen3-4b", m, False) for m in (1, 3, 4, 8, 512, 2048, 8192)]
@@ -566,6 +626,9 @@ def main() -> int:
     ap.add_argument("--ship-gate", action="store_true",
                     help="the reference's microbench ship gate (fused <= eager at M = 1, 5, 8 "
                          "on Qwen3-4B QKV and gate-up); prints one JSON line")
+    ap.add_argument("--profile-set", action="store_true",
+                    help="the fixed kernel sequence the profiles/ summaries other than the "
+                         "default bench's are taken from (one JSON line per entry)")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time the read-only probe (the decode kernels' memory pattern, no "
                          "arithmetic) on the decode weight buffers; prints one JSON line")
@@ -602,6 +665,9 @@ def main() -> int:
         return 0
     if args.configs:
         configs_run(torch, kern, args.steps)
+        return 0
+    if args.profile_set:
+        profile_set_run(torch, kern, args.steps)
         return 0
     if args.read_ceiling:
         print(json.dumps(read_ceiling_run(torch, kern, args.steps)), flush=True)
