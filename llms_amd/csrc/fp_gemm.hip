@@ -460,37 +460,78 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
       W8 ? (uint32_t)(ra * BK + ((((grp >> 1) ^ swz8(ra)) * 16) | ((grp & 1) * 8)))
          : (uint32_t)(ra * BK * 2 + ((grp ^ swzk<BK>(ra)) * 16));
   const uint32_t offb = (uint32_t)(rb * BK * 2 + ((grp ^ swzk<BK>(rb)) * 16));
-  auto compute = [&](const uint16_t (*tw)[WKE], const uint16_t (*tx)[BK]) {
+  static_assert(BK == 64, "two 32-wide k-halves per k-step");
+  // One k-half's MFMA operands as read from LDS: the weight fragments (raw
+  // int8 for W8, dequantised at use) and the x fragments.
+  struct Frag {
+    typename std::conditional<W8, u32x2, u32x4>::type a[FN];
+    u32x4 b[FM];
+  };
+  auto rd_a = [&](Frag& f, const uint16_t (*tw)[WKE], int kk, int i) {
+    const uint32_t oa = offa ^ (uint32_t)(kk * (W8 ? 32 : 64));
+    if constexpr (W8)
+      f.a[i] = *reinterpret_cast<const u32x2*>((const char*)tw + oa + i * 16 * BK);
+    else
+      f.a[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * BK * 2);
+  };
+  auto rd_b = [&](Frag& f, const uint16_t (*tx)[BK], int kk, int j) {
+    const uint32_t ob = offb ^ (uint32_t)(kk * 64);
+    f.b[j] = *reinterpret_cast<const u32x4*>((const char*)tx + ob + j * 16 * BK * 2);
+  };
+  // Wave tiles of up to 24 MFMA blocks (192 x 256) keep the plain loop: all
+  // of a k-half's reads, then its MFMAs (measured on MI355X, 4B QKV at M =
+  // 2048: 60.1 us against 61.6 pipelined; gate-up 320 x 256 175.7 -> 169.5).
+  constexpr bool kPipe = FN * FM > 24;
+  // The MFMAs of k-half f, with the LDS reads of the next k-half (tw, tx,
+  // kk) into g spread between them: weight fragment i right after the last
+  // MFMA that reads f's fragment i, x fragment j right after the last MFMA
+  // that reads f's fragment j (the last row), so g takes f's registers as
+  // they free up. A wave's LDS latency hides under its own MFMAs instead of
+  // stalling the k-half's first MFMA, and the waves' reads no longer arrive
+  // in one burst. With RD false: the MFMAs alone.
+  auto mma = [&](auto RD, const Frag& f, Frag& g, const uint16_t (*tw)[WKE],
+                 const uint16_t (*tx)[BK], int kk) {
+    constexpr bool rd = decltype(RD)::value;
+    if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
-      const uint32_t oa = offa ^ (uint32_t)(kk * (W8 ? 32 : 64)), ob = offb ^ (uint32_t)(kk * 64);
-      u32x4 fa[FN], fb[FM];
+    for (int i = 0; i < FN; ++i) {
+      u32x4 fa;
+      if constexpr (W8)
+        fa = dequant8_bf16(f.a[i].x, f.a[i].y, sc[i], nsc[i]);
+      else
+        fa = f.a[i];
 #pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        if constexpr (W8) {
-          const u32x2 q = *reinterpret_cast<const u32x2*>((const char*)tw + oa + i * 16 * BK);
-          fa[i] = dequant8_bf16(q.x, q.y, sc[i], nsc[i]);
-        } else {
-          fa[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * BK * 2);
-        }
+      for (int j = 0; j < FM; ++j) {
+        acc[i][j] = mfma16(fa, f.b[j], acc[i][j]);
+        if constexpr (rd)
+          if (i == FN - 1) rd_b(g, tx, kk, j);
       }
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-        fb[j] = *reinterpret_cast<const u32x4*>((const char*)tx + ob + j * 16 * BK * 2);
-      if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int j = 0; j < FM; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
-      if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(0);
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (rd) rd_a(g, tw, kk, i);
     }
+    if constexpr (rd) {
+#pragma unroll
+      for (int i = 0; i < FN - 1; ++i) {
+        if constexpr (W8) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, FM, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      if constexpr (W8) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
   };
   auto stw = [&](int st) -> uint16_t (*)[WKE] { return st == 0 ? sW0 : sW1; };
   auto stx = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sX0 : sX1; };
 
   const bool y16 = ((a.ldy & 7) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
   const int64_t nkt = a.K / BK;
+  Frag F, G;
   setup(b);
   issue(sW0, sX0, 0);
   while (true) {
@@ -501,20 +542,55 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     // this tile's first k-step (and the previous tile's output stores)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
-    // k-step k lives in stage k % 2; the loads of step k + 1 are in flight
-    // while step k is consumed (the loop shape of gemm_kernel: with a
-    // different one the compiler double-buffers the accumulators and spills)
-    for (int64_t kt = 0; kt < nkt; kt += 2) {
+    if constexpr (kPipe) {
+      if (nkt > 1) issue(sW1, sX1, BK);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int64_t k = kt + u;
-        if (k >= nkt) break;
-        if (k + 1 < nkt) issue(stw((u + 1) % 2), stx((u + 1) % 2), (k + 1) * BK);
-        compute(stw(u), stx(u));
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        __syncthreads();
+      for (int j = 0; j < FM; ++j) rd_b(F, sX0, 0, j);
+#pragma unroll
+      for (int i = 0; i < FN; ++i) rd_a(F, sW0, 0, i);
+      // k-step k lives in stage k % 2. Its first half's MFMAs run while its
+      // second half is read; then one barrier (every wave is done reading
+      // stage k % 2, and the loads of step k + 1 have landed) lets step
+      // k + 2's loads into that stage, and the second half's MFMAs run while
+      // the first half of step k + 1 is read (on the last step: stale reads,
+      // unused). (The loop shape of gemm_kernel: with a different one the
+      // compiler double-buffers the accumulators and spills.)
+      for (int64_t kt = 0; kt < nkt; kt += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int64_t k = kt + u;
+          if (k >= nkt) break;
+          mma(std::true_type{}, F, G, stw(u), stx(u), 1);
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+          __syncthreads();
+          if (k + 2 < nkt) issue(stw(u), stx(u), (k + 2) * BK);
+          mma(std::true_type{}, G, F, stw(u ^ 1), stx(u ^ 1), 0);
+        }
+      }
+    } else {
+      // k-step k lives in stage k % 2; the loads of step k + 1 are in flight
+      // while step k is consumed, a k-half's reads before its MFMAs
+      for (int64_t kt = 0; kt < nkt; kt += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int64_t k = kt + u;
+          if (k >= nkt) break;
+          if (k + 1 < nkt) issue(stw((u + 1) % 2), stx((u + 1) % 2), (k + 1) * BK);
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int i = 0; i < FN; ++i) rd_a(F, stw(u), kk, i);
+#pragma unroll
+            for (int j = 0; j < FM; ++j) rd_b(F, stx(u), kk, j);
+            mma(std::false_type{}, F, G, sW0, sX0, kk);
+          }
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+          __syncthreads();
+        }
       }
     }
+    // Both loops: the k-steps in gemm_kernel's order and the same MFMA
+    // sequence, so the outputs are bit-identical to it.
     const int bnext = b + gx;
     const bool more = bnext < t_end;
     const int64_t em0 = m0, ec0 = c0;
