@@ -62,7 +62,8 @@ constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >>
 // per k-step in LDS (16 rows per load instruction, chunk c of row r at
 // c ^ ((r >> 2) & 3)); each lane turns the 8 int8 of its MFMA A fragment into
 // bf16(q * s) in registers (dequant8_bf16: the dequantise-then-matmul
-// rounding) before the bf16 MFMA.
+// rounding) before the bf16 MFMA. (The one-tile-per-CU kernel below
+// dequantises once per workgroup instead.)
 template <int BN, int BM, int WN, int WM, bool GATEUP, int NS, bool SPLIT = false, bool W8 = false,
           int BK = kBK>
 __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int n_mt, int n_nt,
@@ -352,6 +353,16 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 //     accumulator layout gives, cost 2x the time at the end of a tile);
 //   - the gate-up epilogue converts two outputs per v_cvt_pk_bf16_f32
 //     (gate_up_silu_pair).
+// int8 weights (W8) are dequantised once per workgroup, not per fragment
+// read: the raw rows of k-step k + 1 land by DMA in a staging buffer (two,
+// 64 B per row each), and during the first half of step k every lane turns
+// its 16-byte chunks into bf16(q * s) in the operand stage of step k + 1, as
+// the dequantise-then-matmul path rounds them; the MFMAs then read bf16
+// fragments exactly as for bf16 weights. Against dequantising each fragment
+// in every wave that reads it (2-4x the VALU work, more than the MFMA time),
+// 4B QKV at M = 2048 (192 x 256) 77.1 -> 60.8 us, gate-up (256 x 256 plus a
+// 256 x 128 tail) 210.5 -> 203 us. The staging needs BN x 128 B of LDS more,
+// so 320 x 256 (184 KB) is bf16 only.
 // Same k-steps in the same order as gemm_kernel: bit-identical outputs.
 // Measured on MI355X against gemm_kernel (4 weight sets cycled): 4B QKV M =
 // 2048 (192 x 256) 60.6 -> 54.7 us, M = 8192 (256 x 256) 215.7 -> 210.3 us;
@@ -366,25 +377,32 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   constexpr int TN = BN / WN, TM = BM / WM;
   constexpr int FN = TN / 16, FM = TM / 16;
   constexpr int WB = W8 ? 1 : 2;
-  constexpr int WKE = BK * WB / 2;
-  constexpr int WRPI = W8 ? 16 : RPI;
-  constexpr int WCPR = W8 ? 4 : CPR;
+  constexpr int WRPI = W8 ? 16 : RPI;         // weight rows per load instruction
+  constexpr int WCPR = W8 ? 4 : CPR;          // 16-byte chunks per weight row
   constexpr int NWI = BN / WRPI;
   constexpr int IW = (NWI + NW - 1) / NW;
   constexpr int IX = BM / RPI / NW;
+  constexpr int NQC = BN * 4;                 // int8: 16-byte chunks per k-step
+  constexpr int QCH = (NQC + NW * kWave - 1) / (NW * kWave);  // ... per lane
   constexpr int TNO = GATEUP ? TN / 2 : TN;   // output columns per wave
   constexpr int SROW = TNO + 8;               // LDS strip row stride (elements)
   constexpr int CPRO = TNO / 8;               // 16-byte chunks per strip row
+  static_assert(BK == 64, "two 32-wide k-halves per k-step");
   static_assert(BN % WRPI == 0 && BM % (RPI * NW) == 0, "tile/waves");
   static_assert(W8 || NWI % NW == 0, "bf16 weight loads spread evenly over the waves");
+  static_assert(NQC % kWave == 0, "int8 chunks: whole waves");
   static_assert(!GATEUP || TN % 32 == 0, "gate-up needs whole gate/up pairs per wave");
   static_assert(NW * 16 * SROW * 2 <= BM * BK * 2, "epilogue strips fit in one x stage");
   static_assert(TNO % 8 == 0, "whole 16-byte chunks per strip row");
 
-  __shared__ __attribute__((aligned(1024))) uint16_t sW0[BN][WKE];
-  __shared__ __attribute__((aligned(1024))) uint16_t sW1[BN][WKE];
+  // bf16 operand stages (int8 weights are dequantised into sW), and for
+  // int8 the raw weight rows of the next k-steps
+  __shared__ __attribute__((aligned(1024))) uint16_t sW0[BN][BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sW1[BN][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX0[BM][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX1[BM][BK];
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ0[W8 ? BN : 1][BK];
+  __shared__ __attribute__((aligned(1024))) uint8_t sQ1[W8 ? BN : 1][BK];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -404,10 +422,11 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   void* const wptr1 = (void*)(GATEUP ? a.w1 : a.w0);
   const int lrow = lane / CPR, lchunk = lane % CPR;
 
-  // per-tile state: origin, DMA lane offsets and (int8) row scales
+  // per-tile state: origin, DMA lane offsets and (int8) the scales of the
+  // rows this lane dequantises
   int64_t m0 = 0, c0 = 0;
   uint32_t woff[IW], xoff[IX];
-  float sc[W8 ? FN : 1], nsc[W8 ? FN : 1];
+  float qs[W8 ? QCH : 1], qn[W8 ? QCH : 1];
   auto wrow_n = [&](int t) -> int64_t { return GATEUP ? c0 + (t / 32) * 16 + (t % 16) : c0 + t; };
   auto wrow_up = [&](int t) -> bool { return GATEUP && ((t / 16) & 1); };
   auto setup = [&](int bb) {
@@ -422,7 +441,9 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
       const int t = (wave + NW * j) * WRPI + lane / WCPR;
       const int c = lane % WCPR;
       const int64_t ld = wrow_up(t) ? a.ldw1 : a.ldw0;
-      woff[j] = (uint32_t)(wrow_n(t) * ld * WB) + (uint32_t)((c ^ (W8 ? swz8(t) : swzk<BK>(t))) * 16);
+      // int8 rows land unswizzled (the dequantisation pass reads them
+      // linearly); bf16 rows in the fragment-read swizzle
+      woff[j] = (uint32_t)(wrow_n(t) * ld * WB) + (uint32_t)((W8 ? c : c ^ swzk<BK>(t)) * 16);
     }
 #pragma unroll
     for (int j = 0; j < IX; ++j) {
@@ -431,48 +452,62 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     }
     if constexpr (W8) {
 #pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        const int t = wn * TN + 16 * i + li;
-        const int64_t n = wrow_n(t);
-        sc[i] = n < a.N ? (wrow_up(t) ? a.s1 : a.s0)[n] : 0.f;
-        nsc[i] = -128.f * sc[i];
+      for (int c = 0; c < QCH; ++c) {
+        const int r = (wave * kWave + lane + NW * kWave * c) / 4;
+        const int64_t n = wrow_n(r);
+        qs[c] = (r < BN && n < a.N) ? (wrow_up(r) ? a.s1 : a.s0)[n] : 0.f;
+        qn[c] = -128.f * qs[c];
       }
     }
   };
-  auto issue = [&](uint16_t (*tw)[WKE], uint16_t (*tx)[BK], int64_t k0) {
+  // weight rows of k-step k0 / BK: bf16 into an operand stage, int8 into a
+  // staging buffer
+  auto issue_w = [&](void* dst, int64_t k0) {
 #pragma unroll
     for (int j = 0; j < IW; ++j) {
       const int q = wave + NW * j;
       if (q >= NWI) break;  // uniform per wave
       const bool up = wrow_up(q * WRPI);
-      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0, (lds_ptr_t)&tw[q * WRPI][0], woff[j],
-                 (uint32_t)(k0 * WB));
+      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0,
+                 (lds_ptr_t)((char*)dst + q * WRPI * BK * WB), woff[j], (uint32_t)(k0 * WB));
     }
+  };
+  auto issue_x = [&](uint16_t (*tx)[BK], int64_t k0) {
 #pragma unroll
     for (int j = 0; j < IX; ++j)
       load_lds16(a.x, xbytes, (lds_ptr_t)&tx[(wave + NW * j) * RPI][0], xoff[j],
                  (uint32_t)(k0 * 2));
   };
+  // int8: chunk c of this lane (16 weights of row r, k-range 16 q .. 16 q +
+  // 15 of the step) from staging buffer sq to bf16(q * s) in stage tw, in
+  // the bf16 fragment-read swizzle; each weight is dequantised once per
+  // workgroup (as the dequantise-then-matmul path rounds it)
+  auto dq_read = [&](const uint8_t (*sq)[BK], int c) -> u32x4 {
+    const int t = wave * kWave + lane + NW * kWave * c;
+    return *reinterpret_cast<const u32x4*>((const char*)sq + t * 16);
+  };
+  auto dq_write = [&](uint16_t (*tw)[BK], int c, u32x4 v) {
+    const int t = wave * kWave + lane + NW * kWave * c;
+    const int r = t / 4, q = t % 4, sw = swzk<BK>(r);
+    *reinterpret_cast<u32x4*>(&tw[r][((2 * q) ^ sw) * 8]) = dequant8_bf16(v.x, v.y, qs[c], qn[c]);
+    *reinterpret_cast<u32x4*>(&tw[r][((2 * q + 1) ^ sw) * 8]) =
+        dequant8_bf16(v.z, v.w, qs[c], qn[c]);
+  };
+  // chunk c exists in every lane of this wave (uniform)
+  auto dq_has = [&](int c) -> bool { return (wave + NW * c) * kWave < NQC; };
 
   f32x4 acc[FN][FM];
   const int ra = wn * TN + li, rb = wm * TM + li;
-  const uint32_t offa =
-      W8 ? (uint32_t)(ra * BK + ((((grp >> 1) ^ swz8(ra)) * 16) | ((grp & 1) * 8)))
-         : (uint32_t)(ra * BK * 2 + ((grp ^ swzk<BK>(ra)) * 16));
+  const uint32_t offa = (uint32_t)(ra * BK * 2 + ((grp ^ swzk<BK>(ra)) * 16));
   const uint32_t offb = (uint32_t)(rb * BK * 2 + ((grp ^ swzk<BK>(rb)) * 16));
-  static_assert(BK == 64, "two 32-wide k-halves per k-step");
-  // One k-half's MFMA operands as read from LDS: the weight fragments (raw
-  // int8 for W8, dequantised at use) and the x fragments.
+  // One k-half's MFMA operands as read from LDS.
   struct Frag {
-    typename std::conditional<W8, u32x2, u32x4>::type a[FN];
+    u32x4 a[FN];
     u32x4 b[FM];
   };
-  auto rd_a = [&](Frag& f, const uint16_t (*tw)[WKE], int kk, int i) {
-    const uint32_t oa = offa ^ (uint32_t)(kk * (W8 ? 32 : 64));
-    if constexpr (W8)
-      f.a[i] = *reinterpret_cast<const u32x2*>((const char*)tw + oa + i * 16 * BK);
-    else
-      f.a[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * BK * 2);
+  auto rd_a = [&](Frag& f, const uint16_t (*tw)[BK], int kk, int i) {
+    const uint32_t oa = offa ^ (uint32_t)(kk * 64);
+    f.a[i] = *reinterpret_cast<const u32x4*>((const char*)tw + oa + i * 16 * BK * 2);
   };
   auto rd_b = [&](Frag& f, const uint16_t (*tx)[BK], int kk, int j) {
     const uint32_t ob = offb ^ (uint32_t)(kk * 64);
@@ -481,41 +516,53 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   // Wave tiles of up to 24 MFMA blocks (192 x 256) keep the plain loop: all
   // of a k-half's reads, then its MFMAs (measured on MI355X, 4B QKV at M =
   // 2048: 60.1 us against 61.6 pipelined; gate-up 320 x 256 175.7 -> 169.5).
-  constexpr bool kPipe = FN * FM > 24;
+  // int8 always pipelines (its dequantisation pass rides in the MFMA block).
+  constexpr bool kPipe = W8 || FN * FM > 24;
   // The MFMAs of k-half f, with the LDS reads of the next k-half (tw, tx,
   // kk) into g spread between them: weight fragment i right after the last
   // MFMA that reads f's fragment i, x fragment j right after the last MFMA
   // that reads f's fragment j (the last row), so g takes f's registers as
   // they free up. A wave's LDS latency hides under its own MFMAs instead of
   // stalling the k-half's first MFMA, and the waves' reads no longer arrive
-  // in one burst. With RD false: the MFMAs alone.
-  auto mma = [&](auto RD, const Frag& f, Frag& g, const uint16_t (*tw)[WKE],
-                 const uint16_t (*tx)[BK], int kk) {
+  // in one burst. With RD false: the MFMAs alone. With DQ (int8): this
+  // lane's dequantisation of the next k-step's weights from staging buffer
+  // sq into stage dw, its LDS reads at the start and its arithmetic and
+  // writes in the middle of the block.
+  auto mma = [&](auto RD, auto DQ, const Frag& f, Frag& g, const uint16_t (*tw)[BK],
+                 const uint16_t (*tx)[BK], int kk, const uint8_t (*sq)[BK],
+                 uint16_t (*dw)[BK]) {
     constexpr bool rd = decltype(RD)::value;
+    constexpr bool dq = decltype(DQ)::value;
+    u32x4 qv[QCH];
     if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(1);
+    if constexpr (dq) {
+#pragma unroll
+      for (int c = 0; c < QCH; ++c)
+        if (dq_has(c)) qv[c] = dq_read(sq, c);
+    }
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
-      u32x4 fa;
-      if constexpr (W8)
-        fa = dequant8_bf16(f.a[i].x, f.a[i].y, sc[i], nsc[i]);
-      else
-        fa = f.a[i];
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
-        acc[i][j] = mfma16(fa, f.b[j], acc[i][j]);
+        acc[i][j] = mfma16(f.a[i], f.b[j], acc[i][j]);
         if constexpr (rd)
           if (i == FN - 1) rd_b(g, tx, kk, j);
       }
       if constexpr (rd) rd_a(g, tw, kk, i);
+      if constexpr (dq) {
+        if (i == FN / 2) {
+#pragma unroll
+          for (int c = 0; c < QCH; ++c)
+            if (dq_has(c)) dq_write(dw, c, qv[c]);
+        }
+      }
     }
-    if constexpr (rd) {
+    if constexpr (rd && !dq) {
 #pragma unroll
       for (int i = 0; i < FN - 1; ++i) {
-        if constexpr (W8) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, FM, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      if constexpr (W8) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -526,14 +573,26 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto stw = [&](int st) -> uint16_t (*)[WKE] { return st == 0 ? sW0 : sW1; };
+  auto stw = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sW0 : sW1; };
   auto stx = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sX0 : sX1; };
+  auto stq = [&](int st) -> uint8_t (*)[BK] { return st == 0 ? sQ0 : sQ1; };
+  // a tile's first loads: k-step 0 into stage 0 (int8: the weights of steps
+  // 0 and 1 into the staging buffers)
+  const int64_t nkt = a.K / BK;
+  auto issue_first = [&]() {
+    issue_x(sX0, 0);
+    if constexpr (W8) {
+      issue_w(sQ0, 0);
+      if (nkt > 1) issue_w(sQ1, BK);
+    } else {
+      issue_w(sW0, 0);
+    }
+  };
 
   const bool y16 = ((a.ldy & 7) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
-  const int64_t nkt = a.K / BK;
   Frag F, G;
   setup(b);
-  issue(sW0, sX0, 0);
+  issue_first();
   while (true) {
 #pragma unroll
     for (int i = 0; i < FN; ++i)
@@ -543,28 +602,51 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
     if constexpr (kPipe) {
-      if (nkt > 1) issue(sW1, sX1, BK);
+      if constexpr (W8) {
+        // step 0's weights into stage 0, then staging buffer 0 takes step 2
+#pragma unroll
+        for (int c = 0; c < QCH; ++c)
+          if (dq_has(c)) dq_write(sW0, c, dq_read(sQ0, c));
+        __syncthreads();
+        if (nkt > 2) issue_w(sQ0, 2 * BK);
+        if (nkt > 1) issue_x(sX1, BK);
+      } else {
+        if (nkt > 1) {
+          issue_x(sX1, BK);
+          issue_w(sW1, BK);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < FM; ++j) rd_b(F, sX0, 0, j);
 #pragma unroll
       for (int i = 0; i < FN; ++i) rd_a(F, sW0, 0, i);
       // k-step k lives in stage k % 2. Its first half's MFMAs run while its
-      // second half is read; then one barrier (every wave is done reading
-      // stage k % 2, and the loads of step k + 1 have landed) lets step
-      // k + 2's loads into that stage, and the second half's MFMAs run while
-      // the first half of step k + 1 is read (on the last step: stale reads,
-      // unused). (The loop shape of gemm_kernel: with a different one the
-      // compiler double-buffers the accumulators and spills.)
+      // second half is read (int8: and step k + 1's weights are dequantised
+      // from staging buffer (k + 1) % 2 into stage (k + 1) % 2; on the last
+      // step stale bytes into a stage nothing reads); then one barrier
+      // (every wave is done reading stage k % 2 and staging buffer
+      // (k + 1) % 2, and the loads of step k + 1 have landed) lets step
+      // k + 2's loads into that stage (int8: step k + 3's weights into that
+      // staging buffer), and the second half's MFMAs run while the first
+      // half of step k + 1 is read (on the last step: stale reads, unused).
+      // (The loop shape of gemm_kernel: with a different one the compiler
+      // double-buffers the accumulators and spills.)
       for (int64_t kt = 0; kt < nkt; kt += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int64_t k = kt + u;
           if (k >= nkt) break;
-          mma(std::true_type{}, F, G, stw(u), stx(u), 1);
+          mma(std::true_type{}, std::integral_constant<bool, W8>{}, F, G, stw(u), stx(u), 1,
+              stq(u ^ 1), stw(u ^ 1));
           __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
           __syncthreads();
-          if (k + 2 < nkt) issue(stw(u), stx(u), (k + 2) * BK);
-          mma(std::true_type{}, G, F, stw(u ^ 1), stx(u ^ 1), 0);
+          if (k + 2 < nkt) {
+            issue_x(stx(u), (k + 2) * BK);
+            if constexpr (!W8) issue_w(stw(u), (k + 2) * BK);
+          }
+          if constexpr (W8)
+            if (k + 3 < nkt) issue_w(stq(u ^ 1), (k + 3) * BK);
+          mma(std::true_type{}, std::false_type{}, G, F, stw(u ^ 1), stx(u ^ 1), 0, sQ0, sW0);
         }
       }
     } else {
@@ -575,14 +657,17 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
         for (int u = 0; u < 2; ++u) {
           const int64_t k = kt + u;
           if (k >= nkt) break;
-          if (k + 1 < nkt) issue(stw((u + 1) % 2), stx((u + 1) % 2), (k + 1) * BK);
+          if (k + 1 < nkt) {
+            issue_w(stw((u + 1) % 2), (k + 1) * BK);
+            issue_x(stx((u + 1) % 2), (k + 1) * BK);
+          }
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
             for (int i = 0; i < FN; ++i) rd_a(F, stw(u), kk, i);
 #pragma unroll
             for (int j = 0; j < FM; ++j) rd_b(F, stx(u), kk, j);
-            mma(std::false_type{}, F, G, sW0, sX0, kk);
+            mma(std::false_type{}, std::false_type{}, F, G, sW0, sX0, kk, sQ0, sW0);
           }
           __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
           __syncthreads();
@@ -590,15 +675,15 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
       }
     }
     // Both loops: the k-steps in gemm_kernel's order and the same MFMA
-    // sequence, so the outputs are bit-identical to it.
+    // sequence on the same bf16 operands, so the outputs are bit-identical
+    // to it.
     const int bnext = b + gx;
     const bool more = bnext < t_end;
     const int64_t em0 = m0, ec0 = c0;
     if (more) {
       setup(bnext);
-      issue(sW0, sX0, 0);
+      issue_first();
     }
-
     // ---- epilogue: per wave, 16 x rows at a time through its strip ----
     uint16_t* strip = &sX1[0][0] + wave * 16 * SROW;
     const int64_t nw0 = ec0 + wn * TNO;  // first output column of this wave
@@ -983,6 +1068,10 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
     if (GATEUP) t.w1 = static_cast<const uint16_t*>(a.w1) + p.nmain * a.ldw1;
   }
   t.y = a.y + p.nmain;
+  // int8 gate-up tails: 256 x 128 tiles of the dequantise-once tile kernel
+  // (the 128 x 128 gemm_kernel dequantises each weight fragment in every
+  // wave that reads it)
+  if constexpr (W8 && GATEUP) return launch_tiles_cfg<256, 128, 4, 2, true, true>(t, s);
   return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, W8>(t, s);
 }
 

@@ -84,19 +84,25 @@ inline bool splitk8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (M < min_m || M > kSplitkMaxM8 || K % 64 != 0) return false;
   return M <= 64 || K <= 8192;
 }
-// Whether an int8 call of this shape runs gemm_kernel with in-register
+// Whether an int8 call of this shape runs the MFMA tiles with in-register
 // dequantisation in preference to dequantising the weights into a workspace
 // first. Measured on MI355X (Qwen3-4B/8B): gate-up from 129 to 1024 rows (8B
-// at 256 rows: 121.7 -> 75.9 us), one weight stream of more than 4096 rows
-// with K <= 2560 from 129 to 512 rows (4B QKV at 256: 33.7 -> 28.4 us). With
-// more rows the dequantisation's VALU work costs 6-12% against the bf16 path
-// on dequantised weights; the long-K down projections keep that path with k
-// split across workgroups. Without a workspace every aligned int8 call of
-// more than 128 rows runs gemm_kernel.
+// at 256 rows: 121.7 -> 75.9 us); one weight stream of more than 4096 rows
+// with K <= 2560 from 129 to 512 rows (4B QKV at 256: 33.7 -> 28.4 us), and
+// where its tiles are one round of 192 x 256 tiles on at least 3/4 of the
+// CUs (the one-tile-per-CU kernel, which dequantises each weight once per
+// workgroup: 4B QKV at 2048 rows 65.2 -> 60.8 us, bf16 60.3). Elsewhere with
+// more rows the dequantisation costs 4-16% against the bf16 path on
+// dequantised weights (4B QKV at 1024 rows 48.5 vs 50.6 us, 8B QKV at 4096
+// 176 vs 204, 4B gate-up at 2048 187 vs 203); the long-K down projections
+// keep that path with k split across workgroups. Without a workspace every
+// aligned int8 call of more than 128 rows runs the in-register tiles.
 inline bool gemm8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (M <= kSplitkMaxM8 || K % 64 != 0) return false;
   if (gateup) return M <= 1024;
-  return N > 4096 && K <= 2560 && M <= 512;
+  if (N <= 4096 || K > 2560) return false;
+  const int64_t tiles192 = ((N + 191) / 192) * ((M + 255) / 256);
+  return M <= 512 || (tiles192 >= 192 && tiles192 <= 256);
 }
 template <bool GATEUP, bool W8>
 int launch_splitk(const StreamArgs& a, hipStream_t s);
