@@ -34,21 +34,41 @@ __global__ __launch_bounds__(256) void quantize_w8_kernel(const uint16_t* w, int
   }
 }
 
-// bf16(q * s[row]) for 16 weights per thread (K % 16 == 0, 16-byte-aligned
-// rows): the weight the int8 kernels compute with, written as a bf16 matrix
-// [N, K] (row stride K) for the bf16 MFMA path.
-__global__ __launch_bounds__(256) void dequant_w8_kernel(const int8_t* q, int64_t ldq,
-                                                         const float* scale, uint16_t* w,
+// bf16(q * s[row]) (K % 16 == 0, 16-byte-aligned rows): the weight the int8
+// kernels compute with, written as a bf16 matrix [N, K] (row stride K) for
+// the bf16 MFMA path. blockIdx.y picks the matrix (gate-up: Wg, Wu in one
+// launch); each thread converts two 16-weight chunks, half the matrix apart,
+// reading the int8 bytes (used once) with the non-temporal hint. Measured on
+// MI355X, 4B gate-up (2 x 9728 x 2560): two launches of one chunk per thread
+// 2 x 15.6 us.
+__global__ __launch_bounds__(256) void dequant_w8_kernel(const int8_t* q0, int64_t ldq0,
+                                                         const float* s0, uint16_t* w0,
+                                                         const int8_t* q1, int64_t ldq1,
+                                                         const float* s1, uint16_t* w1,
                                                          int64_t N, int64_t K) {
-  const int64_t per_row = K / 16;
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= N * per_row) return;
-  const int64_t r = t / per_row, c = (t - r * per_row) * 16;
-  const u32x4 v = ld16(q + r * ldq + c);
-  const float sc = scale[r], n128 = -128.f * sc;
-  uint16_t* out = w + r * K + c;
-  *reinterpret_cast<u32x4*>(out) = dequant8_bf16(v.x, v.y, sc, n128);
-  *reinterpret_cast<u32x4*>(out + 8) = dequant8_bf16(v.z, v.w, sc, n128);
+  const bool second = blockIdx.y != 0;
+  const int8_t* q = second ? q1 : q0;
+  const int64_t ldq = second ? ldq1 : ldq0;
+  const float* scale = second ? s1 : s0;
+  uint16_t* w = second ? w1 : w0;
+  const int64_t per_row = K / 16, total = N * per_row, half = (total + 1) / 2;
+  const int64_t t0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t0 >= half) return;
+  const int64_t t1 = t0 + half;
+  const bool two = t1 < total;
+  const int64_t r0 = t0 / per_row, c0 = (t0 - r0 * per_row) * 16;
+  const int64_t r1 = two ? t1 / per_row : r0, c1 = two ? (t1 - r1 * per_row) * 16 : c0;
+  const u32x4 v0 = ld16_nt(q + r0 * ldq + c0);
+  const u32x4 v1 = ld16_nt(q + r1 * ldq + c1);
+  const float sc0 = scale[r0], sc1 = scale[r1];
+  uint16_t* out0 = w + r0 * K + c0;
+  *reinterpret_cast<u32x4*>(out0) = dequant8_bf16(v0.x, v0.y, sc0, -128.f * sc0);
+  *reinterpret_cast<u32x4*>(out0 + 8) = dequant8_bf16(v0.z, v0.w, sc0, -128.f * sc0);
+  if (two) {
+    uint16_t* out1 = w + r1 * K + c1;
+    *reinterpret_cast<u32x4*>(out1) = dequant8_bf16(v1.x, v1.y, sc1, -128.f * sc1);
+    *reinterpret_cast<u32x4*>(out1 + 8) = dequant8_bf16(v1.z, v1.w, sc1, -128.f * sc1);
+  }
 }
 
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -122,12 +142,11 @@ int run_w8(const StreamArgs& a, bool aligned, void* ws, int64_t ws_bytes, hipStr
   } else if (aligned && use_dequant(a.M, a.N, a.K, GATEUP) && ws && ws_bytes >= wb) {
     uint16_t* w0 = (uint16_t*)ws;
     uint16_t* w1 = GATEUP ? (uint16_t*)((char*)ws + wb / 2) : nullptr;
-    const unsigned blocks = (unsigned)((a.N * (a.K / 16) + 255) / 256);
-    hipLaunchKernelGGL(dequant_w8_kernel, dim3(blocks), dim3(256), 0, s, (const int8_t*)a.w0,
-                       a.ldw0, a.s0, w0, a.N, a.K);
-    if constexpr (GATEUP)
-      hipLaunchKernelGGL(dequant_w8_kernel, dim3(blocks), dim3(256), 0, s, (const int8_t*)a.w1,
-                         a.ldw1, a.s1, w1, a.N, a.K);
+    const unsigned blocks = (unsigned)(((a.N * (a.K / 16) + 1) / 2 + 255) / 256);
+    hipLaunchKernelGGL(dequant_w8_kernel, dim3(blocks, GATEUP ? 2 : 1), dim3(256), 0, s,
+                       (const int8_t*)a.w0, a.ldw0, a.s0, w0,
+                       (const int8_t*)(GATEUP ? a.w1 : a.w0), GATEUP ? a.ldw1 : a.ldw0,
+                       GATEUP ? a.s1 : a.s0, GATEUP ? w1 : w0, a.N, a.K);
     int rc = (int)hipGetLastError();
     if (rc) return launch_status(rc);
     StreamArgs b = a;
