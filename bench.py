@@ -793,6 +793,10 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gu_gbs / PEAK_HBM_GBS, 4),
             "traffic": profiled_traffic(),
+            # not measured in this run: FETCH_SIZE + WRITE_SIZE (copy-
+            # calibrated) of the same kernel and workload from the committed
+            # rocprofv3 --pmc summary of the profiled build
+            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, os.path.dirname(TRAFFIC_PROFILE) + "/.."),
             "algorithmic_bytes": gate_up_bytes(1, K, inter),
             "avg_launch_us": round(d_gu * 1e6, 3),
         },

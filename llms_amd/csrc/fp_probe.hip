@@ -4,8 +4,9 @@
 //
 // The kernel reads a weight-shaped buffer exactly as the row-streaming decode
 // kernel (fp_rows.hip) does — a wave owns whole rows of `row_bytes`, reads
-// each 1 KB run with one 16-byte load per lane, all of a row's runs in flight
-// from the first instruction, 8 waves per workgroup — and does nothing with
+// each 1 KB run with one 16-byte load per lane (with the non-temporal hint,
+// as those kernels load weights), all of a row's runs in flight from the
+// first instruction, 8 waves per workgroup — and does nothing with
 // the data but fold it into one word per wave (so the loads stay live). Its
 // duration is the floor for a launch that streams that many bytes in that
 // pattern: launch, first-byte latency, the HBM stream and the drain.
@@ -29,8 +30,9 @@ __global__ __launch_bounds__(512) void read_rows_kernel(const uint8_t* p0, const
   u32x4 v[U], w[PAIR ? U : 1];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    v[u] = *reinterpret_cast<const u32x4*>(p0 + off + u * 1024);
-    if constexpr (PAIR) w[u] = *reinterpret_cast<const u32x4*>(p1 + off + u * 1024);
+    v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p0 + off + u * 1024));
+    if constexpr (PAIR)
+      w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p1 + off + u * 1024));
   }
   uint32_t x = 0;
 #pragma unroll
