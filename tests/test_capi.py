@@ -372,3 +372,49 @@ def test_padded_strides_on_prefill_tiles(kind, M, K, N):
         out = ref.ref_linear(bits(x)[r], bits(w))
     p = ref.check_parity(bits(yc[:, :N].contiguous())[r], out)
     assert p.ok, (kind, M, p)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,M", [("qkv", 2048), ("gate-up", 2048), ("gate-up", 1300)])
+def test_int8_tiles_dequantise_once(kind, M):
+    """The one-tile-per-CU kernel with int8 weights (each weight dequantised
+    once per workgroup into LDS) on Qwen3-4B shapes, through the plain entry
+    points (no workspace): QKV at 2048 rows is one round of 192 x 256 tiles,
+    gate-up runs whole rounds of 256 x 256 tiles plus a 256 x 128 tail. The
+    same k order as the bf16 kernels, so the outputs equal the bf16 call on
+    the dequantised weights bit for bit; a row subset is checked against the
+    oracle as well."""
+    from llms_amd import _lib
+    from llms_amd import kernels as kern
+
+    K, n_q, n_k, inter = 2560, 4096, 1024, 9728
+    lib = _lib.capi()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows = np.sort(np.random.default_rng(5).choice(M, 48, replace=False))
+    if kind == "qkv":
+        N = n_q + 2 * n_k
+        x, w = qkv_inputs(900 + M, M, K, n_q, n_k)
+        xd = x.cuda()
+        q, s = kern.quantize_w8_per_row(w.cuda())
+        y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        st = lib.fp_qkv_w8(_p(xd), K, _p(q), K, _p(s), _p(y), N, M, n_q, n_k, K, stream)
+        assert st == 0, _lib.status_string(st)
+        wd = kern.dequantize_w8(q, s)
+        yb = torch.cat(kern.triton_fused_qkv(xd, wd, n_q=n_q, n_k=n_k), dim=-1)
+        out = ref.ref_qkv_w8_full(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy(), n_q, n_k)
+    else:
+        x, wg, wu = ffn_inputs(900 + M, M, K, inter)
+        xd = x.cuda()
+        qg, sg = kern.quantize_w8_per_row(wg.cuda())
+        qu, su = kern.quantize_w8_per_row(wu.cuda())
+        y = torch.empty(M, inter, dtype=torch.bfloat16, device="cuda")
+        st = lib.fp_gate_up_silu_w8(_p(xd), K, _p(qg), K, _p(sg), _p(qu), K, _p(su), _p(y), inter,
+                                    M, inter, K, stream)
+        assert st == 0, _lib.status_string(st)
+        yb = kern.triton_fused_gate_up_silu(xd, kern.dequantize_w8(qg, sg), kern.dequantize_w8(qu, su))
+        out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                           qu.cpu().numpy(), su.cpu().numpy())
+    torch.cuda.synchronize()
+    assert torch.equal(y, yb.reshape(M, -1)), f"{kind} M={M}: int8 tiles differ from bf16 on bf16(q*s)"
+    p = ref.check_parity(bits(y.cpu())[rows], out)
+    assert p.ok, (kind, M, p)
