@@ -375,19 +375,22 @@ def test_padded_strides_on_prefill_tiles(kind, M, K, N):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind,M", [("qkv", 2048), ("gate-up", 2048), ("gate-up", 1300)])
-def test_int8_tiles_dequantise_once(kind, M):
+@pytest.mark.parametrize("kind,M,K", [("qkv", 2048, 2560), ("gate-up", 2048, 2560),
+                                      ("gate-up", 1300, 2560), ("gate-up", 2048, 64),
+                                      ("gate-up", 2048, 192), ("qkv", 2048, 128)])
+def test_int8_tiles_dequantise_once(kind, M, K):
     """The one-tile-per-CU kernel with int8 weights (each weight dequantised
     once per workgroup into LDS) on Qwen3-4B shapes, through the plain entry
     points (no workspace): QKV at 2048 rows is one round of 192 x 256 tiles,
     gate-up runs whole rounds of 256 x 256 tiles plus a 256 x 128 tail. The
     same k order as the bf16 kernels, so the outputs equal the bf16 call on
     the dequantised weights bit for bit; a row subset is checked against the
-    oracle as well."""
+    oracle as well. K of 64, 128 and 192 gives tiles of 1, 2 and 3 k-steps
+    (the dequantisation one step ahead reads stale staging on the last)."""
     from llms_amd import _lib
     from llms_amd import kernels as kern
 
-    K, n_q, n_k, inter = 2560, 4096, 1024, 9728
+    n_q, n_k, inter = 4096, 1024, 9728
     lib = _lib.capi()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     rows = np.sort(np.random.default_rng(5).choice(M, 48, replace=False))

@@ -760,3 +760,32 @@ def test_against_torch_gpu_path():
         p_theirs = ref.check_parity(bits(theirs), out)
         print(f"M={M} ours: {p_ours}\nM={M} torch-gpu: {p_theirs}")
         assert p_ours.ok
+
+
+# ----- persistent tile loops with few k-steps ---------------------------------
+
+
+@pytest.mark.parametrize("K", [64, 128, 192, 320])
+def test_tile_loops_few_ksteps(K):
+    """The one-tile-per-CU kernels at 2048 rows with 1, 2, 3 and 5 k-steps of
+    64: the pipelined loop (gate-up, 320 x 256 and int8 256 x 256 tiles: the
+    last step's reads of the next stage are stale and unused, odd step counts
+    end inside the unrolled pair) and the plain loop (QKV, 192 x 256; int8
+    QKV pipelined with its dequantisation one step ahead)."""
+    M, N, n_q, n_k = 2048, 9728, 4096, 1024
+    check_qkv(1700 + K, M, K, n_q, n_k, label=f"qkv M={M} K={K}")
+    check_ffn(1800 + K, M, K, N, label=f"gate-up M={M} K={K}")
+    kern = _kernels()
+    rows = _rows(M, limit=64)
+    x, w = qkv_inputs(1900 + K, M, K, n_q, n_k)
+    q, s = _quant(w)
+    y = torch.cat(kern.fused_qkv_w8(x.to(DEV), q, s, n_q=n_q, n_k=n_k), dim=-1).cpu()
+    _check(y[rows], ref.ref_qkv_w8_full(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy(), n_q, n_k),
+           f"int8 qkv M={M} K={K}")
+    x, wg, wu = ffn_inputs(2000 + K, M, K, N)
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+    _check(y[rows], ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                                 qu.cpu().numpy(), su.cpu().numpy()),
+           f"int8 gate-up M={M} K={K}")
