@@ -115,21 +115,30 @@ def test_prefill_calls_replay_in_graph():
     with 128-wide k-steps (384 rows), gate-up on 320 x 256 tiles (2048 rows),
     a down projection split across workgroups (fp32 partials in a workspace
     from the graph's pool, then the reduce) and an int8 down projection split
-    the same way — replay bit-identically to the eager calls, several times,
-    with eager work between the replays."""
+    the same way, int8 QKV at 2048 rows (one round of tiles that dequantise
+    in LDS) and int8 gate-up at 2048 rows (both matrices dequantised into a
+    workspace from the graph's pool in one launch, then the bf16 tiles) —
+    replay bit-identically to the eager calls, several times, with eager work
+    between the replays."""
     from llms_amd import kernels as K
     from tests._util import ffn_inputs, qkv_inputs
 
     xq, wq = qkv_inputs(31, 384, 2560, 4096, 1024)
     xg, wg, wu = ffn_inputs(32, 2048, 2560, 9728)
     xd, wdn = qkv_inputs(33, 512, 9728, 2560, 0)
-    xq, wq, xg, wg, wu, xd, wdn = (t.to(DEV) for t in (xq, wq, xg, wg, wu, xd, wdn))
+    xq2, _ = qkv_inputs(34, 2048, 2560, 0, 0)
+    xq, wq, xg, wg, wu, xd, wdn, xq2 = (t.to(DEV) for t in (xq, wq, xg, wg, wu, xd, wdn, xq2))
     q8, s8 = K.quantize_w8_per_row(wdn)
+    qq, sq = K.quantize_w8_per_row(wq)
+    qg, sg = K.quantize_w8_per_row(wg)
+    qu, su = K.quantize_w8_per_row(wu)
 
     def calls():
         q, k, v = K.triton_fused_qkv(xq, wq, n_q=4096, n_k=1024)
+        q2, k2, v2 = K.fused_qkv_w8(xq2, qq, sq, n_q=4096, n_k=1024)
         return [q, k, v, K.triton_fused_gate_up_silu(xg, wg, wu),
-                K.fused_linear(xd, wdn), K.fused_linear_w8(xd, q8, s8)]
+                K.fused_linear(xd, wdn), K.fused_linear_w8(xd, q8, s8), q2, k2, v2,
+                K.fused_gate_up_silu_w8(xg, qg, sg, qu, su)]
 
     eager = [t.clone() for t in calls()]
     torch.cuda.synchronize()
