@@ -367,6 +367,21 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 // Measured on MI355X against gemm_kernel (4 weight sets cycled): 4B QKV M =
 // 2048 (192 x 256) 60.6 -> 54.7 us, M = 8192 (256 x 256) 215.7 -> 210.3 us;
 // 4B gate-up M = 8192 711 -> 683 us.
+// Four waves (WN x WM = 2 x 2, one wave per SIMD, bf16, an even number of
+// k-steps): a wave tile of 96 x 128 reads 30% fewer fragment bytes from LDS
+// than the 8-wave 96 x 64, but its 192 accumulators per lane need AGPRs.
+// Through the MFMA builtin the compiler then splits them between AGPRs and
+// VGPRs and copies them back and forth every k-step (or spills); issued by
+// inline asm with the accumulators as "+a" operands they stay in AGPRs, and
+// the k loop is the 8-wave one without its odd-count exit (which made the
+// compiler double-buffer the fragments). The assembler cannot see what the
+// asm statements write, so the accumulators' first and last accesses
+// around them are separated by explicit s_nop (24 wait states, more than a
+// 16x16x32 MFMA's result latency). Gate-up 192 x 256, bit-identical: 4B M =
+// 512 66.3 -> 62.9 us, M = 500 x 9700 70.4 -> 65.2, 8B M = 512 99.9 -> 95.4;
+// with 16 k-steps (0.6B, M = 2048) 29.4 -> 30.1, so four waves need at least
+// 32. QKV 192 x 256 at M = 2048 was even (61.0 us) and the 256 x 256 forms
+// slower, so only gate-up 192 x 256 runs with four waves.
 template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8>
 __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs a, int n_mt,
                                                                     int n_nt) {
@@ -516,8 +531,10 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   // Wave tiles of up to 24 MFMA blocks (192 x 256) keep the plain loop: all
   // of a k-half's reads, then its MFMAs (measured on MI355X, 4B QKV at M =
   // 2048: 60.1 us against 61.6 pipelined; gate-up 320 x 256 175.7 -> 169.5).
-  // int8 always pipelines (its dequantisation pass rides in the MFMA block).
-  constexpr bool kPipe = W8 || FN * FM > 24;
+  // int8 always pipelines (its dequantisation pass rides in the MFMA block),
+  // and so do the four-wave tiles.
+  constexpr bool kPipe = W8 || FN * FM > 24 || NW == 4;
+  static_assert(NW == 8 || (NW == 4 && !W8), "eight waves, or four for bf16");
   // The MFMAs of k-half f, with the LDS reads of the next k-half (tw, tx,
   // kk) into g spread between them: weight fragment i right after the last
   // MFMA that reads f's fragment i, x fragment j right after the last MFMA
@@ -544,7 +561,12 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
-        acc[i][j] = mfma16(f.a[i], f.b[j], acc[i][j]);
+        if constexpr (NW == 4)
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                       : "+a"(acc[i][j])
+                       : "v"(f.a[i]), "v"(f.b[j]));
+        else
+          acc[i][j] = mfma16(f.a[i], f.b[j], acc[i][j]);
         if constexpr (rd)
           if (i == FN - 1) rd_b(g, tx, kk, j);
       }
@@ -589,6 +611,23 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     }
   };
 
+  // Four waves: a wait between the accumulators' accesses on either side of
+  // it and the MFMA asm statements. The empty asm statements tie every
+  // earlier write (the zeroing) to before the s_nop and every later read
+  // (an MFMA's or the epilogue's) to after it; asm volatile statements keep
+  // their order, so the 24 wait states also separate the asm MFMAs issued
+  // before from any read after.
+  auto agpr_fence = [&]() {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) asm volatile("" : "+a"(acc[i][j]));
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) asm volatile("" : "+a"(acc[i][j]));
+  };
   const bool y16 = ((a.ldy & 7) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
   Frag F, G;
   setup(b);
@@ -598,6 +637,8 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // four waves: the zeroed AGPRs settle before an MFMA reads them
+    if constexpr (NW == 4) agpr_fence();
     // this tile's first k-step (and the previous tile's output stores)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     __syncthreads();
@@ -631,6 +672,24 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
       // half of step k + 1 is read (on the last step: stale reads, unused).
       // (The loop shape of gemm_kernel: with a different one the compiler
       // double-buffers the accumulators and spills.)
+      if constexpr (NW == 4) {
+        // the same steps for an even nkt (the launcher checks), without the
+        // odd-count exit
+        for (int64_t kt = 0; kt < nkt; kt += 2) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int64_t k = kt + u;
+            mma(std::true_type{}, std::false_type{}, F, G, stw(u), stx(u), 1, sQ0, sW0);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();
+            if (k + 2 < nkt) {
+              issue_x(stx(u), (k + 2) * BK);
+              issue_w(stw(u), (k + 2) * BK);
+            }
+            mma(std::true_type{}, std::false_type{}, G, F, stw(u ^ 1), stx(u ^ 1), 0, sQ0, sW0);
+          }
+        }
+      } else
       for (int64_t kt = 0; kt < nkt; kt += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -674,6 +733,8 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
         }
       }
     }
+    // four waves: the last MFMAs' results land before the epilogue reads them
+    if constexpr (NW == 4) agpr_fence();
     // Both loops: the k-steps in gemm_kernel's order and the same MFMA
     // sequence on the same bf16 operands, so the outputs are bit-identical
     // to it.
@@ -1044,7 +1105,12 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
   switch (p.tile) {
     case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3, W8>(a, s);
     case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, W8>(a, s);
-    case kT192x256: return launch_tiles_cfg<192, 256, 2, 4, GATEUP, W8>(a, s);
+    case kT192x256:
+      // bf16 gate-up with an even number of at least 32 k-steps: four waves
+      if constexpr (GATEUP && !W8)
+        if ((a.K / kBK) % 2 == 0 && a.K / kBK >= 32)
+          return launch_tiles_cfg<192, 256, 2, 2, true, false>(a, s);
+      return launch_tiles_cfg<192, 256, 2, 4, GATEUP, W8>(a, s);
     default: break;
   }
   if (p.nmain == 0) return launch_tiles_cfg<256, 256, 4, 2, GATEUP, W8>(a, s);

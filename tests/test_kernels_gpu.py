@@ -333,6 +333,27 @@ def test_prefill_rows_independent_of_grid_plan(kind):
         assert torch.equal(ym.view(torch.int16), y[:M].view(torch.int16)), f"{kind} M={M}"
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (512, 2560, 9728),    # Qwen3-4B: 192 x 256 tiles with four waves
+    (500, 2560, 9700),    # the same, partial tiles in M and N
+    (512, 4096, 12288),   # Qwen3-8B: four waves, 64 k-steps
+    (2048, 1024, 3072),   # Qwen3-0.6B, 16 k-steps: eight waves
+    (512, 2496, 9728)])   # 39 k-steps (odd): eight waves
+def test_gate_up_four_wave_tiles(M, K, N):
+    """bf16 gate-up calls planned on 192 x 256 tiles run four waves per
+    workgroup (accumulators in AGPRs) when the k-step count is even and at
+    least 32, else eight: both against the oracle, and repeated calls
+    bit-identical (the tile order and the k order do not depend on timing)."""
+    x, wg, wu = ffn_inputs(230 + M, M, K, N)
+    xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+    y = _kernels().triton_fused_gate_up_silu(xd, wgd, wud).cpu()
+    rows = _rows(M)
+    _check(y[rows], ref.ref_gate_up_silu_full(bits(x)[rows], bits(wg), bits(wu)),
+           f"gate-up 192 x 256 M={M} K={K} N={N}")
+    y2 = _kernels().triton_fused_gate_up_silu(xd, wgd, wud).cpu()
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+
+
 @pytest.mark.parametrize("M", [17, 64, 65, 100, 256])
 def test_regime_boundaries(M):
     """Around the streaming / tiled switch and partial M tiles."""
