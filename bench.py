@@ -544,61 +544,108 @@ CONFIGS = ([("qwen3-0.6b", 1, False)]
            + [("qwen3-8b", m, q) for q in (False, True) for m in (1, 4, 16, 64, 256, 4096)])
 
 
-def configs_run(torch, kern, reps: int):
-    """Both fused projections on every BASELINE configuration, one JSON line
-    each: average launch duration by graph replay over distinct weight sets
-    (36 for M <= 64, else enough to pass the Infinity Cache), GB/s of
-    algorithmic bytes and TFLOP/s; for bf16, torch's F.linear (hipBLASLt) on
-    the same contraction (one GEMM over [Wq; Wk; Wv] or [Wg; Wu], no epilogue)
+def config_line(torch, kern, shape, M: int, int8: bool, reps: int, hipblaslt: bool = True) -> dict:
+    """Both fused projections of one shape (K, n_q, n_k, I) at M rows: average
+    launch duration by graph replay over distinct weight sets (36 for M <= 64,
+    else enough to pass the Infinity Cache), GB/s of algorithmic bytes and
+    TFLOP/s; for bf16 with `hipblaslt`, torch's F.linear (hipBLASLt) on the
+    same contraction (one GEMM over [Wq; Wk; Wv] or [Wg; Wu], no epilogue)
     for scale."""
     import torch.nn.functional as F
 
+    K, n_q, n_k, inter = shape
+    n = n_q + 2 * n_k
+    wbytes = (1 if int8 else 2) * K * (n + 2 * inter)
+    sets = 36 if M <= 64 else max(4, min(36, (1200 << 20) // wbytes))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+
+    def w(rows):
+        return (torch.randn(rows, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+
+    ws = []
+    for _ in range(sets):
+        t = (w(n), w(inter), w(inter))
+        ws.append(tuple(kern.quantize_w8_per_row(v) for v in t) if int8 else t)
+        del t
+    if int8:
+        qk = [lambda t=t: kern.fused_qkv_w8(x, t[0][0], t[0][1], n_q=n_q, n_k=n_k) for t in ws]
+        gu = [lambda t=t: kern.fused_gate_up_silu_w8(x, t[1][0], t[1][1], t[2][0], t[2][1])
+              for t in ws]
+    else:
+        qk = [lambda t=t: kern.triton_fused_qkv(x, t[0], n_q=n_q, n_k=n_k) for t in ws]
+        gu = [lambda t=t: kern.triton_fused_gate_up_silu(x, t[1], t[2]) for t in ws]
+    tq = kernel_seconds(torch, qk, reps)
+    tg = kernel_seconds(torch, gu, reps)
+    wb = 1 if int8 else 2
+    bq = wb * n * K + (4 * n if int8 else 0) + 2 * M * K + 2 * M * n
+    bg = wb * 2 * inter * K + (8 * inter if int8 else 0) + 2 * M * K + 2 * M * inter
+    out = {"M": M, "weights": "int8" if int8 else "bf16", "weight_sets": sets,
+           "qkv_us": round(tq * 1e6, 2), "qkv_gbs": round(bq / tq / 1e9, 1),
+           "qkv_tflops": round(2 * M * K * n / tq / 1e12, 1),
+           "gate_up_us": round(tg * 1e6, 2), "gate_up_gbs": round(bg / tg / 1e9, 1),
+           "gate_up_tflops": round(2 * M * K * 2 * inter / tg / 1e12, 1)}
+    if hipblaslt and not int8:
+        cat_q = [t[0] for t in ws]
+        cat_g = [torch.cat([t[1], t[2]]) for t in ws]
+        out["hipblaslt_qkv_us"] = round(
+            kernel_seconds(torch, [lambda c=c: F.linear(x, c) for c in cat_q], reps) * 1e6, 2)
+        out["hipblaslt_gate_up_us"] = round(
+            kernel_seconds(torch, [lambda c=c: F.linear(x, c) for c in cat_g], reps) * 1e6, 2)
+        del cat_g
+    del ws, qk, gu
+    torch.cuda.empty_cache()
+    return out
+
+
+def configs_run(torch, kern, reps: int):
+    """Both fused projections on every BASELINE configuration, one JSON line
+    each (config_line)."""
     for model, M, int8 in CONFIGS:
-        K, n_q, n_k, inter = SHAPES[model]
-        n = n_q + 2 * n_k
-        wbytes = (1 if int8 else 2) * K * (n + 2 * inter)
-        sets = 36 if M <= 64 else max(4, min(36, (1200 << 20) // wbytes))
-        g = torch.Generator(device="cuda")
-        g.manual_seed(0)
-        x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
-
-        def w(rows):
-            return (torch.randn(rows, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
-
-        ws = []
-        for _ in range(sets):
-            t = (w(n), w(inter), w(inter))
-            ws.append(tuple(kern.quantize_w8_per_row(v) for v in t) if int8 else t)
-            del t
-        if int8:
-            qk = [lambda t=t: kern.fused_qkv_w8(x, t[0][0], t[0][1], n_q=n_q, n_k=n_k) for t in ws]
-            gu = [lambda t=t: kern.fused_gate_up_silu_w8(x, t[1][0], t[1][1], t[2][0], t[2][1])
-                  for t in ws]
-        else:
-            qk = [lambda t=t: kern.triton_fused_qkv(x, t[0], n_q=n_q, n_k=n_k) for t in ws]
-            gu = [lambda t=t: kern.triton_fused_gate_up_silu(x, t[1], t[2]) for t in ws]
-        tq = kernel_seconds(torch, qk, reps)
-        tg = kernel_seconds(torch, gu, reps)
-        wb = 1 if int8 else 2
-        bq = wb * n * K + (4 * n if int8 else 0) + 2 * M * K + 2 * M * n
-        bg = wb * 2 * inter * K + (8 * inter if int8 else 0) + 2 * M * K + 2 * M * inter
-        out = {"mode": "config", "model": model, "M": M, "weights": "int8" if int8 else "bf16",
-               "weight_sets": sets,
-               "qkv_us": round(tq * 1e6, 2), "qkv_gbs": round(bq / tq / 1e9, 1),
-               "qkv_tflops": round(2 * M * K * n / tq / 1e12, 1),
-               "gate_up_us": round(tg * 1e6, 2), "gate_up_gbs": round(bg / tg / 1e9, 1),
-               "gate_up_tflops": round(2 * M * K * 2 * inter / tg / 1e12, 1)}
-        if not int8:
-            cat_q = [t[0] for t in ws]
-            cat_g = [torch.cat([t[1], t[2]]) for t in ws]
-            out["hipblaslt_qkv_us"] = round(
-                kernel_seconds(torch, [lambda c=c: F.linear(x, c) for c in cat_q], reps) * 1e6, 2)
-            out["hipblaslt_gate_up_us"] = round(
-                kernel_seconds(torch, [lambda c=c: F.linear(x, c) for c in cat_g], reps) * 1e6, 2)
-            del cat_g
+        out = {"mode": "config", "model": model}
+        out.update(config_line(torch, kern, SHAPES[model], M, int8, reps))
         print(json.dumps(out), flush=True)
-        del ws, qk, gu
-        torch.cuda.empty_cache()
+
+
+# Per-GPU shards of tensor parallelism: QKV column-parallel by heads (n_q /
+# tp query and n_k / tp key/value columns), gate-up column-parallel over I
+# with Wg and Wu split alike. The rows each GPU computes at the M of the
+# decode, verify and prefill configurations.
+SHARD_TP = (2, 4, 8)
+SHARD_M = (1, 4, 8, 512, 2048)
+
+
+def shard_shape(model: str, tp: int):
+    K, n_q, n_k, inter = SHAPES[model]
+    return (K, n_q // tp, n_k // tp, inter // tp)
+
+
+def shards_run(torch, kern, reps: int):
+    """Both fused projections on the per-GPU shard of TP = 2, 4, 8 for
+    Qwen3-4B and -8B (one JSON line per model, tp and M), with the layer
+    pair's time and its fraction of the HBM (M <= 8) or MFMA (M >= 512)
+    peak. One GPU runs one shard: what it shows is each GPU's share of a TP
+    layer, without the all-reduce that follows o and down."""
+    for model in ("qwen3-4b", "qwen3-8b"):
+        for tp in SHARD_TP:
+            shape = shard_shape(model, tp)
+            K, n_q, n_k, inter = shape
+            for M in SHARD_M:
+                out = {"mode": "shard", "model": model, "tp": tp, "K": K,
+                       "n_qkv": n_q + 2 * n_k, "I": inter}
+                out.update(config_line(torch, kern, shape, M, False, reps))
+                pair_us = out["qkv_us"] + out["gate_up_us"]
+                out["pair_us"] = round(pair_us, 2)
+                if M <= 8:
+                    gbs = pair_bytes(M, K, n_q + 2 * n_k, inter) / pair_us / 1e3
+                    out["pair_gbs"] = round(gbs, 1)
+                    out["frac_of_peak"] = round(gbs / PEAK_HBM_GBS, 4)
+                else:
+                    tf = pair_flops(M, K, n_q + 2 * n_k, inter) / pair_us / 1e6
+                    out["pair_tflops"] = round(tf, 1)
+                    out["frac_of_peak"] = round(tf / PEAK_BF16_TFLOPS, 4)
+                print(json.dumps(out), flush=True)
 
 
 def main() -> int:
@@ -623,6 +670,9 @@ def main() -> int:
     ap.add_argument("--configs", action="store_true",
                     help="time both projections on every BASELINE configuration (with "
                          "hipBLASLt for scale); one JSON line per configuration")
+    ap.add_argument("--shards", action="store_true",
+                    help="time both projections on the per-GPU shards of TP = 2, 4, 8 "
+                         "(Qwen3-4B and -8B); one JSON line per shard and M")
     ap.add_argument("--ship-gate", action="store_true",
                     help="the reference's microbench ship gate (fused <= eager at M = 1, 5, 8 "
                          "on Qwen3-4B QKV and gate-up); prints one JSON line")
@@ -665,6 +715,9 @@ def main() -> int:
         return 0
     if args.configs:
         configs_run(torch, kern, args.steps)
+        return 0
+    if args.shards:
+        shards_run(torch, kern, args.steps)
         return 0
     if args.profile_set:
         profile_set_run(torch, kern, args.steps)

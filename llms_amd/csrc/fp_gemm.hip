@@ -381,7 +381,8 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 // 512 66.3 -> 62.9 us, M = 500 x 9700 70.4 -> 65.2, 8B M = 512 99.9 -> 95.4;
 // with 16 k-steps (0.6B, M = 2048) 29.4 -> 30.1, so four waves need at least
 // 32. QKV 192 x 256 at M = 2048 was even (61.0 us) and the 256 x 256 forms
-// slower, so only gate-up 192 x 256 runs with four waves.
+// slower, so of the 192 x 256 tiles only gate-up runs with four waves; the
+// 192 x 128 tile (96 accumulators per lane) has four waves only.
 template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8>
 __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs a, int n_mt,
                                                                     int n_nt) {
@@ -915,14 +916,14 @@ bool gemm_supported(const StreamArgs& a, bool aligned, bool w8) {
 // kK*: bf16 tiles with 128-wide k-steps (two LDS stages: 64 KB, 112 KB and
 // 128 KB).
 enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256, kT192x256,
-                kK64x64, kK96x128, kK128x128, kT320x256 };
+                kK64x64, kK96x128, kK128x128, kT320x256, kT192x128 };
 struct TileInfo {
   int bn, bm, per_cu;
 };
 constexpr TileInfo kTiles[] = {{64, 32, 4},   {128, 64, 3},  {64, 128, 2},
                                {128, 128, 2}, {256, 256, 1}, {192, 256, 1},
                                {64, 64, 2},   {96, 128, 1},  {128, 128, 1},
-                               {320, 256, 1}};
+                               {320, 256, 1}, {192, 128, 1}};
 constexpr int kCUs = 256;
 
 int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
@@ -1083,6 +1084,16 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf
   const auto per_cu = [&](int t) { return (tile_count(t, M, N, gateup) + kCUs - 1) / kCUs; };
   if (best.tile == kT128x128 && per_cu(kT128x128) == 1 && per_cu(kT64x128) <= 2)
     best = GemmPlan{kT64x128, 0};
+  // A single round of 192 x 128 tiles with four waves (accumulators in
+  // AGPRs), one per CU on at least 240 CUs, with an even number of at least
+  // 32 k-steps: faster than the plan above wherever measured on MI355X (µs,
+  // previous plan -> 192 x 128): 8B gate-up M = 256 80.8 -> 73.3, gate-up
+  // 4096 -> 2 x 6144 at M = 512 73.7 -> 67.0 and 4096 -> 2 x 1536 at M =
+  // 2048 66.1 -> 63.7, QKV 2560 -> 3072 at M = 2048 47.7 -> 44.2 and 4096 ->
+  // 3072 at M = 2048 66.8 -> 62.9. At 204-208 tiles it was 6% faster once and
+  // 9% slower once, at 128 or fewer up to 46% slower.
+  const int64_t n192 = tile_count(kT192x128, M, N, gateup);
+  if (bf16 && nkt % 2 == 0 && nkt >= 32 && n192 >= 240 && n192 <= kCUs) best = GemmPlan{kT192x128, 0};
   return best;
 }
 
@@ -1105,6 +1116,9 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
   switch (p.tile) {
     case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3, W8>(a, s);
     case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, W8>(a, s);
+    case kT192x128:
+      if constexpr (!W8) return launch_tiles_cfg<192, 128, 2, 2, GATEUP, false>(a, s);
+      return (int)hipErrorInvalidValue;  // never planned for int8
     case kT192x256:
       // bf16 gate-up with an even number of at least 32 k-steps: four waves
       if constexpr (GATEUP && !W8)

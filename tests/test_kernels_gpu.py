@@ -354,6 +354,47 @@ def test_gate_up_four_wave_tiles(M, K, N):
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
 
 
+@pytest.mark.parametrize("case", ["gate-up 8b", "gate-up ragged", "qkv"])
+def test_192x128_four_wave_tiles(case):
+    """Calls planned as one round of 192 x 128 tiles with four waves (240-256
+    tiles): against the oracle on a row subset, and bit-identical to the
+    same rows computed by a larger call on another plan (192 x 256 or 128 x
+    128 tiles: the same k-steps in the same order)."""
+    if case == "qkv":
+        K, n_q, n_k, M, M2 = 2560, 2048, 512, 2048, 1536
+        x, w = qkv_inputs(260, M, K, n_q, n_k)
+        xd, wd = x.to(DEV), w.to(DEV)
+
+        def run(xx):
+            q, k, v = _kernels().triton_fused_qkv(xx, wd, n_q=n_q, n_k=n_k)
+            return torch.cat([q, k, v], dim=-1).cpu()
+        y = run(xd)
+        rows = _rows(M)
+        _check(y[rows], ref.ref_qkv_full(bits(x)[rows], bits(w), n_q, n_k), f"192x128 {case}")
+        y2 = run(xd[:M2].contiguous())
+        assert torch.equal(y2.view(torch.int16), y[:M2].view(torch.int16))
+        return
+    K, N, M, M2 = (4096, 12288, 256, 512) if case == "gate-up 8b" else (4096, 12200, 250, 500)
+    x, wg, wu = ffn_inputs(270 + M, M2, K, N)
+    xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+    y2 = _kernels().triton_fused_gate_up_silu(xd, wgd, wud).cpu()
+    y = _kernels().triton_fused_gate_up_silu(xd[:M].contiguous(), wgd, wud).cpu()
+    rows = _rows(M, limit=96)
+    _check(y[rows], ref.ref_gate_up_silu_full(bits(x)[rows], bits(wg), bits(wu)), f"192x128 {case}")
+    assert torch.equal(y.view(torch.int16), y2[:M].view(torch.int16))
+
+
+@pytest.mark.parametrize("model", ["4b", "8b"])
+@pytest.mark.parametrize("M", [1, 4, 8, 64, 512, 2048])
+def test_tp8_shards(model, M):
+    """The per-GPU shard of TP = 8 (QKV: 4 q heads + 1 k + 1 v head, 768
+    columns; gate-up: I / 8 columns of Wg and of Wu), the shapes one GPU runs
+    in a tensor-parallel layer, against the oracle."""
+    K, n_q, n_k, I = QWEN3_4B if model == "4b" else QWEN3_8B
+    check_qkv(240 + M, M, K, n_q // 8, n_k // 8, label=f"{model} tp8 qkv M={M}")
+    check_ffn(250 + M, M, K, I // 8, label=f"{model} tp8 gate-up M={M}")
+
+
 @pytest.mark.parametrize("M", [17, 64, 65, 100, 256])
 def test_regime_boundaries(M):
     """Around the streaming / tiled switch and partial M tiles."""
