@@ -232,11 +232,14 @@ def cpu_baseline(torch, stacks: dict, reps: int) -> dict:
     }
 
 
-def counters_run(torch, kern, shape, layers: int, Mp: int = 2048) -> dict:
+def counters_run(torch, kern, shape, layers: int, Mp: int = 2048, blt: bool = False) -> dict:
     """A short fixed sequence for `rocprofv3 --pmc` runs: a plain device copy
     of known size (calibrates FETCH_SIZE / WRITE_SIZE), then three passes of
     the decode (M=1) fused kernels over `layers` cycled weight sets and three
-    of the prefill (M=Mp, default 2048) kernels over 4 of them."""
+    of the prefill (M=Mp, default 2048) kernels over 4 of them. With `blt`,
+    then three passes of torch's F.linear (hipBLASLt) on the same prefill
+    contractions (one GEMM over [Wq; Wk; Wv] and one over [Wg; Wu], no
+    epilogue), for a side-by-side profile."""
     K, n_q, n_k, inter = shape
     n_qkv = n_q + 2 * n_k
     copy_bytes = 256 << 20
@@ -256,6 +259,16 @@ def counters_run(torch, kern, shape, layers: int, Mp: int = 2048) -> dict:
             kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k)
             kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l])
     torch.cuda.synchronize()
+    if blt:
+        import torch.nn.functional as F
+
+        cat_g = [torch.cat([stack.wg[l], stack.wu[l]]) for l in range(min(4, layers))]
+        torch.cuda.synchronize()
+        for _ in range(3):
+            for l in range(min(4, layers)):
+                F.linear(stack.x_attn, stack.wqkv[l])
+                F.linear(stack.x_ffn, cat_g[l])
+        torch.cuda.synchronize()
     return {
         "mode": "counters",
         "copy": {"kernel": "bfloat16_copy_kernel", "read_bytes": copy_bytes,
@@ -662,6 +675,9 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--counters", action="store_true",
                     help="run only the short fixed sequence used for rocprofv3 --pmc runs")
+    ap.add_argument("--hipblaslt", action="store_true",
+                    help="with --counters: also run torch's F.linear (hipBLASLt) on the "
+                         "prefill contractions, for a side-by-side profile")
     ap.add_argument("--decode", action="store_true",
                     help="end-to-end decode on a Qwen3-4B-shaped harness model with random "
                          "weights: reference eager path vs fused modules, eager and "
@@ -708,7 +724,8 @@ def main() -> int:
     n_qkv = n_q + 2 * n_k
     L = args.layers
     if args.counters:
-        print(json.dumps(counters_run(torch, kern, shape, L, args.prefill_m)), flush=True)
+        print(json.dumps(counters_run(torch, kern, shape, L, args.prefill_m, args.hipblaslt)),
+              flush=True)
         return 0
     if args.decode:
         print(json.dumps(decode_run(torch, args.decode_tokens)), flush=True)
