@@ -276,6 +276,15 @@ bool splitk_supported(const StreamArgs& a, bool aligned, bool w8) {
 // sets, warm clocks): the x tile is M rounded up to 16 (up to 64 rows), then
 // 64 x 64 tiles; gate-up tiles hold 16 outputs (32 weight rows). int8 (half
 // the bytes per weight row, so more rows of LDS per wave) prefers 8 waves.
+// Narrow bf16 outputs at up to 16 rows with K >= 2560 (the per-GPU shards
+// of tensor parallelism: QKV of at most 2048 columns, gate-up of at most
+// 3072; also 0.6B down) have too few tiles for 256 CUs; 8 waves per tile put
+// twice the k-steps in flight there. Same-box A/B, µs at M = 4 and 8, 4 -> 8
+// waves: 8B QKV 1536 columns 8.1-8.4 -> 6.1-7.0, 768 columns 8.0-8.2 ->
+// 5.6-7.2; 8B gate-up 3072 columns 12.5-12.8 -> 11.0-11.7, 1536 columns
+// 10.7-11.2 -> 8.8-9.6; 4B QKV 768 and 1536 columns 6.0-6.8 -> 4.6-5.9;
+// 0.6B down (1024 x 3072) 6.5-7.0 -> 5.7-6.3. The full Qwen3-4B/8B outputs
+// keep 4 waves (8 were 2-14% slower there).
 template <bool GATEUP, bool W8>
 int launch_splitk(const StreamArgs& a, hipStream_t s) {
   if constexpr (W8 && GATEUP) {
@@ -289,12 +298,16 @@ int launch_splitk(const StreamArgs& a, hipStream_t s) {
     if (a.M <= 64) return launch_splitk_cfg<32, 64, 8, 2, false, true>(a, s);
     return launch_splitk_cfg<64, 64, 4, 2, false, true>(a, s);
   } else if constexpr (GATEUP) {
-    if (a.M <= 16) return launch_splitk_cfg<32, 16, 4, 3, true, W8>(a, s);
+    if (a.M <= 16)
+      return a.N <= 3072 && a.K >= 2560 ? launch_splitk_cfg<32, 16, 8, 2, true, W8>(a, s)
+                         : launch_splitk_cfg<32, 16, 4, 3, true, W8>(a, s);
     if (a.M <= 32) return launch_splitk_cfg<32, 32, 8, 2, true, W8>(a, s);
     if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, true, W8>(a, s);
     return launch_splitk_cfg<64, 64, 4, 2, true, W8>(a, s);
   } else {
-    if (a.M <= 16) return launch_splitk_cfg<16, 16, 4, 3, false, W8>(a, s);
+    if (a.M <= 16)
+      return a.N <= 2048 && a.K >= 2560 ? launch_splitk_cfg<16, 16, 8, 3, false, W8>(a, s)
+                         : launch_splitk_cfg<16, 16, 4, 3, false, W8>(a, s);
     if (a.M <= 32) return launch_splitk_cfg<32, 32, 4, 3, false, W8>(a, s);
     if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, false, W8>(a, s);
     return launch_splitk_cfg<64, 64, 4, 2, false, W8>(a, s);
