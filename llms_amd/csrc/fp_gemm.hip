@@ -383,10 +383,13 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 // 32. QKV 192 x 256 at M = 2048 was even (61.0 us) and the 256 x 256 forms
 // slower, so of the 192 x 256 tiles only gate-up runs with four waves; the
 // 192 x 128 tile (96 accumulators per lane) has four waves only.
-template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8>
+// With four waves the k-step may also be 128 wide (BK = 128: four 32-wide
+// substeps, each one's MFMAs carrying the next one's fragment reads, the
+// barrier before the last), for the one-round grids of 96 x 128 and 128 x
+// 128 tiles that gemm_kernel would run with 128-wide steps.
+template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8, int BK = kBK>
 __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs a, int n_mt,
                                                                     int n_nt) {
-  constexpr int BK = kBK;
   constexpr int NW = WN * WM;
   constexpr int CPR = BK / 8;
   constexpr int RPI = 1024 / (BK * 2);
@@ -403,7 +406,8 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   constexpr int TNO = GATEUP ? TN / 2 : TN;   // output columns per wave
   constexpr int SROW = TNO + 8;               // LDS strip row stride (elements)
   constexpr int CPRO = TNO / 8;               // 16-byte chunks per strip row
-  static_assert(BK == 64, "two 32-wide k-halves per k-step");
+  static_assert(BK == 64 || (BK == 128 && WN * WM == 4 && !W8),
+                "32-wide k-substeps: two per k-step, or four with four bf16 waves");
   static_assert(BN % WRPI == 0 && BM % (RPI * NW) == 0, "tile/waves");
   static_assert(W8 || NWI % NW == 0, "bf16 weight loads spread evenly over the waves");
   static_assert(NQC % kWave == 0, "int8 chunks: whole waves");
@@ -681,6 +685,11 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
           for (int u = 0; u < 2; ++u) {
             const int64_t k = kt + u;
             mma(std::true_type{}, std::false_type{}, F, G, stw(u), stx(u), 1, sQ0, sW0);
+            if constexpr (BK == 128) {
+              // substeps 1 and 2 of the four, each reading the next
+              mma(std::true_type{}, std::false_type{}, G, F, stw(u), stx(u), 2, sQ0, sW0);
+              mma(std::true_type{}, std::false_type{}, F, G, stw(u), stx(u), 3, sQ0, sW0);
+            }
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
             if (k + 2 < nkt) {
@@ -851,14 +860,14 @@ int launch_gemm_cfg(const StreamArgs& a, hipStream_t s) {
 // The persistent form of a one-tile-per-CU grid: one workgroup per CU (at
 // most one per tile).
 constexpr int kTilesGrid = 256;
-template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8 = false>
+template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8 = false, int BK = kBK>
 int launch_tiles_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t cols = GATEUP ? BN / 2 : BN;
   const int n_nt = (int)((a.N + cols - 1) / cols);
   const int n_mt = (int)((a.M + BM - 1) / BM);
   const int64_t tiles = (int64_t)n_nt * n_mt;
   const int grid = tiles < kTilesGrid ? (int)((tiles + 7) / 8 * 8) : kTilesGrid;
-  hipLaunchKernelGGL((gemm_tiles_kernel<BN, BM, WN, WM, GATEUP, W8>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((gemm_tiles_kernel<BN, BM, WN, WM, GATEUP, W8, BK>), dim3((unsigned)grid),
                      dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt);
   return (int)hipGetLastError();
 }
@@ -1106,9 +1115,24 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
         if constexpr (GATEUP) return launch_tiles_cfg<320, 256, 2, 4, true>(a, s);
         return launch_tiles_cfg<320, 256, 4, 2, false>(a, s);
       case kK64x64: return launch_gemm_cfg<64, 64, 2, 2, GATEUP, 2, false, 128>(a, s);
-      case kK128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, false, 128>(a, s);
+      // The one-per-CU tiles with 128-wide k-steps run as the pipelined
+      // four-wave tile loop where their step count is even (measured on
+      // MI355X against gemm_kernel, bit-identical, µs: 4B QKV M = 512 30.9
+      // -> 27.5, M = 384 30.8 -> 27.2; 8B QKV M = 512 44.1 -> 39.8; 0.6B
+      // QKV M = 1024 16.4 -> 14.7, gate-up M = 512 15.7 -> 14.8; other
+      // shapes even). 64 x 64 tiles run two per CU in gemm_kernel, which
+      // one persistent workgroup per CU does not match (0.6B QKV M = 512
+      // 11.9 -> 16.8).
+      case kK128x128:
+        if ((a.K / (2 * kBK)) % 2 == 0)
+          return launch_tiles_cfg<128, 128, 2, 2, GATEUP, false, 2 * kBK>(a, s);
+        return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, false, 128>(a, s);
       case kK96x128:
-        if constexpr (!GATEUP) return launch_gemm_cfg<96, 128, 2, 2, false, 2, false, 128>(a, s);
+        if constexpr (!GATEUP) {
+          if ((a.K / (2 * kBK)) % 2 == 0)
+            return launch_tiles_cfg<96, 128, 2, 2, false, false, 2 * kBK>(a, s);
+          return launch_gemm_cfg<96, 128, 2, 2, false, 2, false, 128>(a, s);
+        }
         return (int)hipErrorInvalidValue;  // never planned for gate-up
       default: break;
     }
