@@ -925,14 +925,16 @@ bool gemm_supported(const StreamArgs& a, bool aligned, bool w8) {
 // kK*: bf16 tiles with 128-wide k-steps (two LDS stages: 64 KB, 112 KB and
 // 128 KB).
 enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256, kT192x256,
-                kK64x64, kK96x128, kK128x128, kT320x256, kT192x128 };
+                kK64x64, kK96x128, kK128x128, kT320x256, kT192x128, kT160x128,
+                kT128x160 };
 struct TileInfo {
   int bn, bm, per_cu;
 };
 constexpr TileInfo kTiles[] = {{64, 32, 4},   {128, 64, 3},  {64, 128, 2},
                                {128, 128, 2}, {256, 256, 1}, {192, 256, 1},
                                {64, 64, 2},   {96, 128, 1},  {128, 128, 1},
-                               {320, 256, 1}, {192, 128, 1}};
+                               {320, 256, 1}, {192, 128, 1}, {160, 128, 1},
+                               {128, 160, 1}};
 constexpr int kCUs = 256;
 
 int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
@@ -1093,16 +1095,28 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf
   const auto per_cu = [&](int t) { return (tile_count(t, M, N, gateup) + kCUs - 1) / kCUs; };
   if (best.tile == kT128x128 && per_cu(kT128x128) == 1 && per_cu(kT64x128) <= 2)
     best = GemmPlan{kT64x128, 0};
-  // A single round of 192 x 128 tiles with four waves (accumulators in
-  // AGPRs), one per CU on at least 240 CUs, with an even number of at least
-  // 32 k-steps: faster than the plan above wherever measured on MI355X (µs,
-  // previous plan -> 192 x 128): 8B gate-up M = 256 80.8 -> 73.3, gate-up
-  // 4096 -> 2 x 6144 at M = 512 73.7 -> 67.0 and 4096 -> 2 x 1536 at M =
-  // 2048 66.1 -> 63.7, QKV 2560 -> 3072 at M = 2048 47.7 -> 44.2 and 4096 ->
-  // 3072 at M = 2048 66.8 -> 62.9. At 204-208 tiles it was 6% faster once and
-  // 9% slower once, at 128 or fewer up to 46% slower.
-  const int64_t n192 = tile_count(kT192x128, M, N, gateup);
-  if (bf16 && nkt % 2 == 0 && nkt >= 32 && n192 >= 240 && n192 <= kCUs) best = GemmPlan{kT192x128, 0};
+  // A single round of four-wave tiles (accumulators in AGPRs) on at least
+  // 240 CUs: 192 x 128, else 128 x 160 or 160 x 128, with an even number of
+  // 128-wide k-steps (192 x 128 also with an even number of at least 32
+  // 64-wide ones). Faster than the plan above wherever measured on MI355X
+  // (µs, previous plan -> 64-wide steps -> 128-wide steps): 8B gate-up M =
+  // 256 80.8 -> 73.4 -> 64.8; gate-up 4096 -> 2 x 6144 at M = 512 73.7 ->
+  // 67.2 -> 56.5, 4096 -> 2 x 1536 at M = 2048 66.1 -> 62.9 -> 52.6; QKV 2560
+  // -> 3072 at M = 2048 47.7 -> 44.3 -> 38.1, 4096 -> 3072 at M = 2048 66.8
+  // -> 63.1 -> 52.7; 128 x 160 for gate-up 2560 -> 2 x 1216 at M = 2048 42.2
+  // -> 32.1; 160 x 128 for gate-up 2560 -> 2 x 4864 at M = 512 52.8 -> 36.3.
+  // At 204-208 tiles 192 x 128 was 6% faster once and 9% slower once
+  // (64-wide steps), at 128 or fewer up to 46% slower.
+  if (bf16) {
+    const bool k128 = K % (2 * kBK) == 0 && (K / (2 * kBK)) % 2 == 0;
+    const auto one_round = [&](int t) {
+      const int64_t n = tile_count(t, M, N, gateup);
+      return n >= 240 && n <= kCUs;
+    };
+    if (one_round(kT192x128) && (k128 || (nkt % 2 == 0 && nkt >= 32))) return GemmPlan{kT192x128, 0};
+    if (k128 && one_round(kT128x160)) return GemmPlan{kT128x160, 0};
+    if (k128 && one_round(kT160x128)) return GemmPlan{kT160x128, 0};
+  }
   return best;
 }
 
@@ -1141,7 +1155,22 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
     case kT64x128: return launch_gemm_cfg<64, 128, 2, 2, GATEUP, 3, W8>(a, s);
     case kT128x128: return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, W8>(a, s);
     case kT192x128:
-      if constexpr (!W8) return launch_tiles_cfg<192, 128, 2, 2, GATEUP, false>(a, s);
+    case kT160x128:
+    case kT128x160:
+      // four waves, 128-wide k-steps where their count is even (planned
+      // only so, except 192 x 128, which may take 64-wide ones)
+      if constexpr (!W8) {
+        const bool k128 = a.K % (2 * kBK) == 0 && (a.K / (2 * kBK)) % 2 == 0;
+        if (p.tile == kT192x128) {
+          if (k128) return launch_tiles_cfg<192, 128, 2, 2, GATEUP, false, 2 * kBK>(a, s);
+          return launch_tiles_cfg<192, 128, 2, 2, GATEUP, false>(a, s);
+        }
+        if (!k128) return (int)hipErrorInvalidValue;  // never planned so
+        if (p.tile == kT128x160) return launch_tiles_cfg<128, 160, 2, 2, GATEUP, false, 2 * kBK>(a, s);
+        // 160 x 128: gate-up needs whole gate/up pairs per wave (one wave column)
+        if constexpr (GATEUP) return launch_tiles_cfg<160, 128, 1, 4, true, false, 2 * kBK>(a, s);
+        return launch_tiles_cfg<160, 128, 2, 2, false, false, 2 * kBK>(a, s);
+      }
       return (int)hipErrorInvalidValue;  // never planned for int8
     case kT192x256:
       // bf16 gate-up with an even number of at least 32 k-steps: four waves

@@ -384,6 +384,45 @@ def test_192x128_four_wave_tiles(case):
     assert torch.equal(y.view(torch.int16), y2[:M].view(torch.int16))
 
 
+@pytest.mark.parametrize("op,M,M2,K,N", [
+    ("gate-up", 2048, 1500, 2560, 1216),  # 128 x 160 tiles; 1500 rows: 128 x 128
+    ("gate-up", 2000, 1500, 2560, 1216),  # 128 x 160, partial last m-tile
+    ("gate-up", 512, 1024, 2560, 4864),   # 160 x 128 (one wave column); 1024 rows: 192 x 256
+    ("qkv", 1024, 768, 2560, 5000),       # 160 x 128; 768 rows: 128 x 128
+    ("qkv", 2048, 1024, 2560, 2432)])     # 128 x 160; 1024 rows: 128 x 128
+def test_four_wave_128_wide_steps(op, M, M2, K, N):
+    """One round of four-wave tiles with 128-wide k-steps (128 x 160 and
+    160 x 128 planned on 240-256 tiles; 128 x 128 one-round grids): against
+    the oracle on a row subset, and bit-identical to the same rows computed
+    on the other plan of a call with M2 rows."""
+    Mx = max(M, M2)
+    if op == "qkv":
+        n_k = N // 6
+        n_q = N - 2 * n_k
+        x, w = qkv_inputs(280 + M, Mx, K, n_q, n_k)
+        xd, wd = x.to(DEV), w.to(DEV)
+
+        def run(rows):
+            q, k, v = _kernels().triton_fused_qkv(xd[:rows].contiguous(), wd, n_q=n_q, n_k=n_k)
+            return torch.cat([q, k, v], dim=-1).cpu()
+        y = run(M)
+        sub = _rows(M)
+        _check(y[sub], ref.ref_qkv_full(bits(x)[sub], bits(w), n_q, n_k), f"{op} M={M} N={N}")
+    else:
+        x, wg, wu = ffn_inputs(290 + M, Mx, K, N)
+        xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+
+        def run(rows):
+            return _kernels().triton_fused_gate_up_silu(xd[:rows].contiguous(), wgd, wud).cpu()
+        y = run(M)
+        sub = _rows(M)
+        _check(y[sub], ref.ref_gate_up_silu_full(bits(x)[sub], bits(wg), bits(wu)),
+               f"{op} M={M} N={N}")
+    y2 = run(M2)
+    r = min(M, M2)
+    assert torch.equal(y[:r].view(torch.int16), y2[:r].view(torch.int16)), f"{op} M={M} vs {M2}"
+
+
 @pytest.mark.parametrize("model", ["4b", "8b"])
 @pytest.mark.parametrize("M", [1, 4, 8, 64, 512, 2048])
 def test_tp8_shards(model, M):
