@@ -170,7 +170,7 @@ int64_t w8_workspace_bytes(int64_t M, int64_t N, int64_t K, bool gateup) {
   const GemmSplit p8 = split8_plan(M, N, K, gateup);
   if (p8.tile >= 0) return 4 * gemm_split_ws_floats(p8, M, N, K, gateup);
   return dequant_bytes(N, K, gateup) +
-         4 * gemm_split_ws_floats(gemm_split_plan(M, N, K, gateup), M, N, K, gateup);
+         4 * gemm_split_ws_floats(gemm_split_plan_bf16(M, N, K, gateup), M, N, K, gateup);
 }
 
 // RMSNorm prologue + projection: one launch on the rows kernel (x normalised
@@ -253,7 +253,7 @@ int fp_abi_version(void) { return (1 << 16) | 4; }
 
 int64_t fp_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up) {
   if (M < 1 || N < 1 || K < 1) return 0;
-  const fp::GemmSplit p = fp::gemm_split_plan(M, N, K, gate_up != 0);
+  const fp::GemmSplit p = fp::gemm_split_plan_bf16(M, N, K, gate_up != 0);
   return 4 * fp::gemm_split_ws_floats(p, M, N, K, gate_up != 0);
 }
 
@@ -390,8 +390,8 @@ int64_t fp_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up,
   if (M <= (w8 ? fp::kRowsMaxM : 2) && K % (w8 ? 16 : 8) == 0 && fp::rows_fit(M, K, w8, true))
     return b;
   if (w8) return b + fp::w8_workspace_bytes(M, N, K, gate_up != 0);
-  return b + 4 * fp::gemm_split_ws_floats(fp::gemm_split_plan(M, N, K, gate_up != 0), M, N, K,
-                                          gate_up != 0);
+  return b + 4 * fp::gemm_split_ws_floats(fp::gemm_split_plan_bf16(M, N, K, gate_up != 0), M, N,
+                                          K, gate_up != 0);
 }
 
 int fp_rmsnorm_qkv_bf16(const void* x, int64_t ldx, const void* gamma, float eps, const void* w,

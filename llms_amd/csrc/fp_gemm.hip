@@ -53,6 +53,8 @@ __device__ __forceinline__ void load_lds16(const void* base, int nbytes, lds_ptr
 
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= v only.
 constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >> 4) << 14); }
+// ... and for lgkmcnt == 0 (every LDS access of this wave done) as well.
+constexpr int vmcnt_lgkm0_imm(int v) { return (v & 15) | (7 << 4) | ((v >> 4) << 14); }
 
 // SPLIT: the grid holds nsplit workgroups per tile, each contracting one
 // contiguous range of k-steps, and the fp32 accumulators go to the workspace
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 // substeps, each one's MFMAs carrying the next one's fragment reads, the
 // barrier before the last), for the one-round grids of 96 x 128 and 128 x
 // 128 tiles that gemm_kernel would run with 128-wide steps.
-template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8, int BK = kBK>
+template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8, int BK = kBK, int NS = 2>
 __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs a, int n_mt,
                                                                     int n_nt) {
   constexpr int NW = WN * WM;
@@ -408,6 +410,7 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   constexpr int CPRO = TNO / 8;               // 16-byte chunks per strip row
   static_assert(BK == 64 || (BK == 128 && WN * WM == 4 && !W8),
                 "32-wide k-substeps: two per k-step, or four with four bf16 waves");
+  static_assert(NS == 2 || (NS == 3 && WN * WM == 4 && !W8), "three LDS stages: four bf16 waves");
   static_assert(BN % WRPI == 0 && BM % (RPI * NW) == 0, "tile/waves");
   static_assert(W8 || NWI % NW == 0, "bf16 weight loads spread evenly over the waves");
   static_assert(NQC % kWave == 0, "int8 chunks: whole waves");
@@ -419,8 +422,10 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   // int8 the raw weight rows of the next k-steps
   __shared__ __attribute__((aligned(1024))) uint16_t sW0[BN][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sW1[BN][BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sW2[NS > 2 ? BN : 1][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX0[BM][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX1[BM][BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sX2[NS > 2 ? BM : 1][BK];
   __shared__ __attribute__((aligned(1024))) uint8_t sQ0[W8 ? BN : 1][BK];
   __shared__ __attribute__((aligned(1024))) uint8_t sQ1[W8 ? BN : 1][BK];
 
@@ -482,20 +487,22 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   };
   // weight rows of k-step k0 / BK: bf16 into an operand stage, int8 into a
   // staging buffer
-  auto issue_w = [&](void* dst, int64_t k0) {
+  // live false: the same instructions with an empty buffer range (they read
+  // nothing and land zeros), so that every step issues the same loads
+  auto issue_w = [&](void* dst, int64_t k0, bool live = true) {
 #pragma unroll
     for (int j = 0; j < IW; ++j) {
       const int q = wave + NW * j;
-      if (q >= NWI) break;  // uniform per wave
+      if (NWI % NW != 0 && q >= NWI) break;  // uniform per wave
       const bool up = wrow_up(q * WRPI);
-      load_lds16(up ? wptr1 : a.w0, up ? wbytes1 : wbytes0,
+      load_lds16(up ? wptr1 : a.w0, live ? (up ? wbytes1 : wbytes0) : 0,
                  (lds_ptr_t)((char*)dst + q * WRPI * BK * WB), woff[j], (uint32_t)(k0 * WB));
     }
   };
-  auto issue_x = [&](uint16_t (*tx)[BK], int64_t k0) {
+  auto issue_x = [&](uint16_t (*tx)[BK], int64_t k0, bool live = true) {
 #pragma unroll
     for (int j = 0; j < IX; ++j)
-      load_lds16(a.x, xbytes, (lds_ptr_t)&tx[(wave + NW * j) * RPI][0], xoff[j],
+      load_lds16(a.x, live ? xbytes : 0, (lds_ptr_t)&tx[(wave + NW * j) * RPI][0], xoff[j],
                  (uint32_t)(k0 * 2));
   };
   // int8: chunk c of this lane (16 weights of row r, k-range 16 q .. 16 q +
@@ -600,8 +607,8 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto stw = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sW0 : sW1; };
-  auto stx = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sX0 : sX1; };
+  auto stw = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sW0 : (st == 1 ? sW1 : sW2); };
+  auto stx = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sX0 : (st == 1 ? sX1 : sX2); };
   auto stq = [&](int st) -> uint8_t (*)[BK] { return st == 0 ? sQ0 : sQ1; };
   // a tile's first loads: k-step 0 into stage 0 (int8: the weights of steps
   // 0 and 1 into the staging buffers)
@@ -661,6 +668,11 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
           issue_x(sX1, BK);
           issue_w(sW1, BK);
         }
+        if constexpr (NS > 2)
+          if (nkt > 2) {
+            issue_x(sX2, 2 * BK);
+            issue_w(sW2, 2 * BK);
+          }
       }
 #pragma unroll
       for (int j = 0; j < FM; ++j) rd_b(F, sX0, 0, j);
@@ -679,24 +691,49 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
       // double-buffers the accumulators and spills.)
       if constexpr (NW == 4) {
         // the same steps for an even nkt (the launcher checks), without the
-        // odd-count exit
-        for (int64_t kt = 0; kt < nkt; kt += 2) {
+        // odd-count exit. With three stages (NS = 3) step k lives in stage
+        // k % 3, the loads of step k + 3 go out after step k's barrier, and
+        // the wait before that barrier leaves step k + 2's loads in flight
+        // (LPS per wave): loads get two steps to land instead of one. Every
+        // step issues its loads, past the last step with an empty range, so
+        // that the compiler's count of loads in flight is exact (it would
+        // otherwise wait for all of them before the next stage's reads).
+        constexpr int LPS = IW + IX;  // load instructions per wave and k-step
+        for (int64_t kt = 0; kt < nkt; kt += NS) {
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
+          for (int u = 0; u < NS; ++u) {
             const int64_t k = kt + u;
+            if constexpr (NS > 2)
+              if (k >= nkt) break;
             mma(std::true_type{}, std::false_type{}, F, G, stw(u), stx(u), 1, sQ0, sW0);
             if constexpr (BK == 128) {
               // substeps 1 and 2 of the four, each reading the next
               mma(std::true_type{}, std::false_type{}, G, F, stw(u), stx(u), 2, sQ0, sW0);
               mma(std::true_type{}, std::false_type{}, F, G, stw(u), stx(u), 3, sQ0, sW0);
             }
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            __syncthreads();
-            if (k + 2 < nkt) {
-              issue_x(stx(u), (k + 2) * BK);
-              issue_w(stw(u), (k + 2) * BK);
+            if constexpr (NS > 2) {
+              // this wave's loads of step k + 1 have landed and its reads of
+              // stage u are done; then a bare barrier (__syncthreads' fence
+              // would wait for every load in flight)
+              if (k + 2 < nkt)
+                __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(LPS));
+              else
+                __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));
+              __builtin_amdgcn_s_barrier();
+            } else {
+              __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+              __syncthreads();
             }
-            mma(std::true_type{}, std::false_type{}, G, F, stw(u ^ 1), stx(u ^ 1), 0, sQ0, sW0);
+            if constexpr (NS > 2) {
+              const bool live = k + NS < nkt;
+              issue_x(stx(u), live ? (k + NS) * BK : 0, live);
+              issue_w(stw(u), live ? (k + NS) * BK : 0, live);
+            } else if (k + NS < nkt) {
+              issue_x(stx(u), (k + NS) * BK);
+              issue_w(stw(u), (k + NS) * BK);
+            }
+            mma(std::true_type{}, std::false_type{}, G, F, stw((u + 1) % NS), stx((u + 1) % NS), 0,
+                sQ0, sW0);
           }
         }
       } else
@@ -745,6 +782,12 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     }
     // four waves: the last MFMAs' results land before the epilogue reads them
     if constexpr (NW == 4) agpr_fence();
+    // three stages: the empty-range loads of the last steps have landed in
+    // every wave before the epilogue strips take stage 1
+    if constexpr (NS > 2) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      __syncthreads();
+    }
     // Both loops: the k-steps in gemm_kernel's order and the same MFMA
     // sequence on the same bf16 operands, so the outputs are bit-identical
     // to it.
@@ -860,14 +903,14 @@ int launch_gemm_cfg(const StreamArgs& a, hipStream_t s) {
 // The persistent form of a one-tile-per-CU grid: one workgroup per CU (at
 // most one per tile).
 constexpr int kTilesGrid = 256;
-template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8 = false, int BK = kBK>
+template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8 = false, int BK = kBK, int NS = 2>
 int launch_tiles_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t cols = GATEUP ? BN / 2 : BN;
   const int n_nt = (int)((a.N + cols - 1) / cols);
   const int n_mt = (int)((a.M + BM - 1) / BM);
   const int64_t tiles = (int64_t)n_nt * n_mt;
   const int grid = tiles < kTilesGrid ? (int)((tiles + 7) / 8 * 8) : kTilesGrid;
-  hipLaunchKernelGGL((gemm_tiles_kernel<BN, BM, WN, WM, GATEUP, W8, BK>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((gemm_tiles_kernel<BN, BM, WN, WM, GATEUP, W8, BK, NS>), dim3((unsigned)grid),
                      dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt);
   return (int)hipGetLastError();
 }
@@ -926,7 +969,7 @@ bool gemm_supported(const StreamArgs& a, bool aligned, bool w8) {
 // 128 KB).
 enum GemmTile { kT64x32, kT128x64, kT64x128, kT128x128, kT256x256, kT192x256,
                 kK64x64, kK96x128, kK128x128, kT320x256, kT192x128, kT160x128,
-                kT128x160 };
+                kT128x160, kT96x64, kT64x128w, kT96x128 };
 struct TileInfo {
   int bn, bm, per_cu;
 };
@@ -934,7 +977,7 @@ constexpr TileInfo kTiles[] = {{64, 32, 4},   {128, 64, 3},  {64, 128, 2},
                                {128, 128, 2}, {256, 256, 1}, {192, 256, 1},
                                {64, 64, 2},   {96, 128, 1},  {128, 128, 1},
                                {320, 256, 1}, {192, 128, 1}, {160, 128, 1},
-                               {128, 160, 1}};
+                               {128, 160, 1}, {96, 64, 1},   {64, 128, 1},  {96, 128, 1}};
 constexpr int kCUs = 256;
 
 int64_t tile_count(int tile, int64_t M, int64_t N, bool gateup) {
@@ -1067,8 +1110,49 @@ bool k128_wide(int64_t M, int64_t N, int64_t K, bool gateup) {
   return n >= kCUs && n * 20 >= K;
 }
 
+// A single round of small four-wave tiles with three LDS stages (bf16,
+// 128-wide k-steps, more than 128 rows): 96 x 64 where at most 256 of them
+// cover the output, else 64 x 128 with 192-256 tiles, either with enough
+// tiles against the k loop: 3 per k-step for gate-up and for up to 24
+// k-steps, 6 per k-step above (fewer leave the call to k split across or
+// inside workgroups); -1 if neither. The third stage gives each k-step's
+// loads two steps to land instead of one, and the small tiles keep three
+// stages within the LDS (120 and 144 KB). Measured on MI355X over Qwen3
+// 0.6B/4B/8B QKV, gate-up, o, down and their tensor-parallel (TP) shards at
+// M = 136..2048 (µs, previous plan -> this; hipBLASLt on the same
+// contraction in brackets): 8B TP=2 QKV 4096 -> 3072 at M = 512 35.4 -> 25.5
+// (24.7); 4B TP=2 QKV 2560 -> 3072 at 512 25.0 -> 18.7 (18.7); 8B TP=8 QKV
+// 4096 -> 768 at 2048 34.1 -> 24.4 (24.4); 8B QKV 4096 -> 6144 at 256 31.7 ->
+// 26.6 (40.1); 8B TP=8 gate-up 4096 -> 2 x 1536 at 512 35.1 -> 25.7 (24.8);
+// 4B TP=4 QKV 2560 -> 1536 at 1024 23.6 -> 17.8; 0.6B o 2048 -> 1024 at 768
+// 17.6 -> 12.7; 0.6B down 3072 -> 1024 at 2048 (64 x 128) 27.5 -> 21.7; 8B
+// o 4096 -> 4096 at 512 (64 x 128) 32.7 -> 27.9. With 32 k-steps and 96-129
+// tiles the split plans were 4-12% faster (8B TP=2 QKV at 192 rows 22.4 vs
+// 25.1, 8B o at 192 23.6 vs 25.4), with 76 k-steps 13% (4B down at 768). The
+// same tiles with two stages: 96 x 64 on 8B TP=2 QKV at 512 32.2, 64 x 128
+// 34.0.
+int small_round_tile(int64_t M, int64_t N, int64_t K, bool gateup) {
+  if (K % (2 * kBK) != 0 || M <= 128) return -1;
+  const int64_t nk = K / (2 * kBK);
+  const int64_t need = (gateup || nk <= 24 ? 3 : 6) * nk;
+  const int64_t n1 = tile_count(kT96x64, M, N, gateup);
+  if (n1 <= kCUs) return n1 >= need ? kT96x64 : -1;
+  const int64_t n2 = tile_count(kT64x128w, M, N, gateup);
+  return n2 >= 192 && n2 <= kCUs && n2 >= need ? kT64x128w : -1;
+}
+
 GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf16) {
   if (bf16) {
+    const int ts = small_round_tile(M, N, K, gateup);
+    if (ts >= 0) return GemmPlan{ts, 0};
+    // gate-up: one round of 96 x 128 four-wave tiles (96 weight rows, 48
+    // outputs; an even number of 128-wide k-steps) on at least 192 CUs:
+    // 8B TP=4 gate-up 4096 -> 2 x 3072 at M = 512 57.6 -> 39.5 us (hipBLASLt
+    // 35.8), 4B TP=4 2560 -> 2 x 2432 at 512 31.2 -> 27.6 (26.8)
+    if (gateup && K % (2 * kBK) == 0 && (K / (2 * kBK)) % 2 == 0) {
+      const int64_t n = tile_count(kT96x128, M, N, true);
+      if (n >= 192 && n <= kCUs) return GemmPlan{kT96x128, 0};
+    }
     const int t = k128_tile(M, N, K, gateup);
     if (t >= 0) return GemmPlan{t, 0};
   }
@@ -1148,6 +1232,22 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
           return launch_gemm_cfg<96, 128, 2, 2, false, 2, false, 128>(a, s);
         }
         return (int)hipErrorInvalidValue;  // never planned for gate-up
+      // Four waves, 128-wide k-steps. 96 x 64 and 64 x 128 with three LDS
+      // stages (any step count); 96 x 128 with two (an even step count).
+      // Gate-up tiles whose weight rows cannot be split into whole gate/up
+      // pairs per wave column take one wave column.
+      case kT96x64:
+        if (a.K % (2 * kBK) != 0) return (int)hipErrorInvalidValue;  // never planned so
+        if constexpr (GATEUP) return launch_tiles_cfg<96, 64, 1, 4, true, false, 2 * kBK, 3>(a, s);
+        return launch_tiles_cfg<96, 64, 2, 2, false, false, 2 * kBK, 3>(a, s);
+      case kT64x128w:
+        if (a.K % (2 * kBK) != 0) return (int)hipErrorInvalidValue;
+        if constexpr (GATEUP) return launch_tiles_cfg<64, 128, 1, 4, true, false, 2 * kBK, 3>(a, s);
+        return launch_tiles_cfg<64, 128, 2, 2, false, false, 2 * kBK, 3>(a, s);
+      case kT96x128:
+        if (a.K % (2 * kBK) != 0 || (a.K / (2 * kBK)) % 2 != 0) return (int)hipErrorInvalidValue;
+        if constexpr (GATEUP) return launch_tiles_cfg<96, 128, 1, 4, true, false, 2 * kBK>(a, s);
+        return launch_tiles_cfg<96, 128, 2, 2, false, false, 2 * kBK>(a, s);
       default: break;
     }
   }
@@ -1267,9 +1367,14 @@ int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K
   return (int64_t)gemm_splitk_used(K, p.nsplit) * M * (gateup ? 2 * N : N);
 }
 
+GemmSplit gemm_split_plan_bf16(int64_t M, int64_t N, int64_t K, bool gateup) {
+  if (small_round_tile(M, N, K, gateup) >= 0) return GemmSplit{-1, 1};
+  return gemm_split_plan(M, N, K, gateup);
+}
+
 bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p) {
   if (!a.ws || !gemm_supported(a, aligned, false)) return false;
-  *p = gemm_split_plan(a.M, a.N, a.K, gateup);
+  *p = gemm_split_plan_bf16(a.M, a.N, a.K, gateup);
   return p->tile >= 0 && gemm_split_ws_floats(*p, a.M, a.N, a.K, gateup) <= a.ws_floats;
 }
 

@@ -125,6 +125,9 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf
 // a tile for every CU and one per 20 columns of K (then it beats the split-K
 // tiles).
 bool k128_wide(int64_t M, int64_t N, int64_t K, bool gateup);
+// The tile of a single round of small three-stage tiles for this bf16 call
+// (a GemmTile of fp_gemm.hip), -1 if none.
+int small_round_tile(int64_t M, int64_t N, int64_t K, bool gateup);
 // k split across workgroups — for calls whose tile grid leaves the chip
 // partly idle while each tile has a long k loop — with fp32 partials in the
 // caller's workspace and a fixed-order reduce (fp_gemm.hip). tile < 0: no
@@ -134,6 +137,10 @@ struct GemmSplit {
   int nsplit;
 };
 GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup);
+// The split of a bf16 call: none where a round of small three-stage tiles
+// (small_round_tile) runs instead. (int8 calls that split on their int8
+// weights keep gemm_split_plan.)
+GemmSplit gemm_split_plan_bf16(int64_t M, int64_t N, int64_t K, bool gateup);
 int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K, bool gateup);
 // Whether the bf16 call a runs split (plan + workspace large enough).
 bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p);

@@ -215,7 +215,8 @@ int launch_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // has a tile for every CU and one per 20 columns of K (k128_wide: Qwen3-4B
 // QKV, 6144 x 2560, at 160-256 rows: 23.0-28.6 -> 17.9-24.4 us; below 160
 // rows, and 8B QKV, 4B o and 0.6B o and down, keep the split-K tiles, up to
-// 20% faster there). int8 shapes that
+// 20% faster there), or unless a round of small three-stage tiles fits
+// (small_round_tile: 8B QKV at 256 rows 31.6 -> 26.8 us). int8 shapes that
 // splitk8_shape() admits run the split-K tiles too, other aligned int8 calls
 // with whole 64-wide k-steps run gemm_kernel (both dequantise in registers);
 // unaligned rows and K tails run tiled_kernel.
@@ -225,7 +226,8 @@ int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s) {
   GemmSplit sp;
   if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP, false>(a, sp, s);
   if (!W8 && a.M <= kSplitkMaxM && wrows <= kSplitkSmallN && a.K >= kSplitkMinKTiled &&
-      splitk_supported(a, aligned, false) && !k128_wide(a.M, a.N, a.K, GATEUP))
+      splitk_supported(a, aligned, false) && !k128_wide(a.M, a.N, a.K, GATEUP) &&
+      small_round_tile(a.M, a.N, a.K, GATEUP) < 0)
     return launch_splitk<GATEUP, false>(a, s);
   if (!W8 && gemm_supported(a, aligned, false)) return launch_gemm<GATEUP, false>(a, s);
   if (W8 && splitk8_shape(a.M, a.N, a.K, GATEUP) && splitk_supported(a, aligned, true))

@@ -50,12 +50,16 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_bytes_plan():
     """The split-k plan (a host function: no GPU needed). Splits only where
-    the unsplit grid leaves the chip idle and k is long: Qwen3 down/o from 32
-    rows, 8B QKV at 256 rows; never for short K, few rows, K % 64 != 0, a
-    chip-filling grid, or where one round of tiles with 128-wide k-steps runs
-    instead with at most 6 splits (4B QKV at 256 rows, 4B o at 640) or 3 (8B o
-    at 1024). The workspace holds one fp32 plane per k range, 2..16 ranges, of
-    M x N (gate-up: M x 2N)."""
+    the unsplit grid leaves the chip idle and k is long: Qwen3 down from 32
+    rows, o at 256 rows, 8B QKV at 128, 8B TP=8 QKV shards (768 columns) at
+    512;
+    never for short K, few rows, K % 64 != 0, a chip-filling grid, where one
+    round of tiles with 128-wide k-steps runs instead with at most 6 splits
+    (4B QKV at 256 rows, 4B o at 640) or 3 (8B o at 1024), or where a round
+    of small three-stage tiles with enough tiles per k-step runs instead (8B
+    QKV at 256 rows, 4B TP=4 QKV shards at 512). The workspace
+    holds one fp32 plane per k range, 2..16 ranges, of M x N (gate-up: M x
+    2N)."""
     from llms_amd import _lib
 
     wb = _lib.capi().fp_workspace_bytes
@@ -69,8 +73,10 @@ def test_workspace_bytes_plan():
     for M in (32, 64, 128, 256, 512, 1024):
         assert 2 <= planes(M, 2560, 9728) <= 16, M          # 4B down
         assert 2 <= planes(M, 4096, 12288) <= 16, M         # 8B down
-    assert 2 <= planes(256, 6144, 4096) <= 16               # 8B QKV, 256 rows
-    assert 2 <= planes(256, 2560, 4096) <= 16               # 4B o, 256 rows (8 splits)
+    assert 2 <= planes(128, 6144, 4096) <= 16               # 8B QKV, 128 rows
+    assert 2 <= planes(128, 2560, 4096) <= 16               # 4B o, 128 rows
+    assert 2 <= planes(256, 2560, 4096) <= 16               # 4B o, 256 rows: 108 small tiles
+    assert 2 <= planes(512, 768, 4096) <= 16                # 8B TP=8 QKV: 64 tiles, 32 k-steps
     assert 2 <= planes(128, 1024, 3072) <= 16               # 0.6B down, few tiles
     assert 2 <= planes(300, 1001, 8192) <= 16                # narrow, ragged N
     assert 2 <= planes(64, 12288, 4096, 1) <= 16             # 8B gate-up, 64 rows
@@ -80,7 +86,8 @@ def test_workspace_bytes_plan():
                  (512, 2560, 9736, 0), (8192, 2560, 9728, 0), (0, 2560, 9728, 0),
                  (512, 0, 9728, 0), (64, 9728, 2560, 1), (32, 12288, 4096, 1),
                  (128, 9728, 2560, 1), (32, 6144, 4096, 0), (256, 6144, 2560, 0),
-                 (640, 2560, 4096, 0), (1024, 4096, 4096, 0)]:
+                 (640, 2560, 4096, 0), (1024, 4096, 4096, 0), (256, 6144, 4096, 0),
+                 (512, 1536, 2560, 0)]:
         assert wb(*args) == 0, args
     # ranges hold at least 8 k-steps of 64
     assert planes(32, 2560, 2048) <= 4
@@ -236,10 +243,10 @@ def test_capi_raw_pointers_match_oracle():
         p = ref.check_parity(bits(y_)[rows], ref.ref_linear(bits(xw)[rows], bits(ww)))
         assert p.ok, p
 
-    # the other workspace variants with the planned workspace (QKV at 256
+    # the other workspace variants with the planned workspace (QKV at 128
     # rows with K = 4096 splits; gate-up here does not, so its workspace is
     # unused)
-    Mq, nq, nk, Kq = 256, 4096, 1024, 4096
+    Mq, nq, nk, Kq = 128, 4096, 1024, 4096
     xq, wq = qkv_inputs(93, Mq, Kq, nq, nk)
     xqd, wqd = xq.cuda(), wq.cuda()
     Nq = nq + 2 * nk
