@@ -493,16 +493,20 @@ def read_ceiling_run(torch, kern, reps: int) -> dict:
 
 
 # The kernel families profiled under profiles/ besides the default bench's
-# decode and prefill grids: (label, model, M, int8, which projections).
+# decode and prefill grids: (label, model, M, int8, tensor-parallel degree of
+# the per-GPU shard, 1 for the whole layer).
 PROFILE_SET = [
-    ("int8 decode", "qwen3-4b", 1, True, "both"),
-    ("int8 verify", "qwen3-4b", 4, True, "both"),
-    ("int8 prefill", "qwen3-4b", 2048, True, "both"),
-    ("bf16 verify M=3", "qwen3-4b", 3, False, "both"),
-    ("bf16 verify M=8", "qwen3-4b", 8, False, "both"),
-    ("split-K tiles M=64", "qwen3-8b", 64, False, "both"),
-    ("split-K tiles M=256", "qwen3-8b", 256, False, "both"),
-    ("prefill M=8192", "qwen3-4b", 8192, False, "both"),
+    ("int8 decode", "qwen3-4b", 1, True, 1),
+    ("int8 verify", "qwen3-4b", 4, True, 1),
+    ("int8 prefill", "qwen3-4b", 2048, True, 1),
+    ("bf16 verify M=3", "qwen3-4b", 3, False, 1),
+    ("bf16 verify M=8", "qwen3-4b", 8, False, 1),
+    ("split-K tiles M=64", "qwen3-8b", 64, False, 1),
+    ("8B M=256", "qwen3-8b", 256, False, 1),
+    ("prefill M=8192", "qwen3-4b", 8192, False, 1),
+    ("8B TP=2 shard M=512", "qwen3-8b", 512, False, 2),
+    ("8B TP=4 shard M=512", "qwen3-8b", 512, False, 4),
+    ("8B TP=8 shard M=512", "qwen3-8b", 512, False, 8),
 ]
 
 
@@ -513,8 +517,8 @@ def profile_set_run(torch, kern, reps: int) -> dict:
     `reps` times after a short warm-up; one JSON line per entry with the
     measured per-launch times."""
     out = {"mode": "profile_set", "entries": []}
-    for label, model, M, int8, _ in PROFILE_SET:
-        K, n_q, n_k, inter = SHAPES[model]
+    for label, model, M, int8, tp in PROFILE_SET:
+        K, n_q, n_k, inter = shard_shape(model, tp)
         n = n_q + 2 * n_k
         wbytes = (1 if int8 else 2) * K * (n + 2 * inter)
         sets = 36 if M <= 64 else max(4, min(36, (1200 << 20) // wbytes))
@@ -536,8 +540,8 @@ def profile_set_run(torch, kern, reps: int) -> dict:
         else:
             qk = [lambda t=t: kern.triton_fused_qkv(x, t[0], n_q=n_q, n_k=n_k) for t in ws]
             gu = [lambda t=t: kern.triton_fused_gate_up_silu(x, t[1], t[2]) for t in ws]
-        ent = {"label": label, "model": model, "M": M, "weights": "int8" if int8 else "bf16",
-               "weight_sets": sets}
+        ent = {"label": label, "model": model, "tp": tp, "M": M,
+               "weights": "int8" if int8 else "bf16", "weight_sets": sets}
         for name, launches in (("qkv", qk), ("gate_up", gu)):
             graph = capture(torch, lambda: [fn() for fn in launches])
             sec = time_graph(torch, graph, reps, 2) / len(launches)

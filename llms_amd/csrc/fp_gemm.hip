@@ -388,10 +388,15 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 // With four waves the k-step may also be 128 wide (BK = 128: four 32-wide
 // substeps, each one's MFMAs carrying the next one's fragment reads, the
 // barrier before the last), for the one-round grids of 96 x 128 and 128 x
-// 128 tiles that gemm_kernel would run with 128-wide steps.
-template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8, int BK = kBK, int NS = 2>
+// 128 tiles that gemm_kernel would run with 128-wide steps; and small tiles
+// may take three or four LDS stages (NS), and then (SPLIT) contract one
+// range of k-steps per work item into fp32 partials for
+// splitk_reduce_kernel, as gemm_kernel's split form does.
+template <int BN, int BM, int WN, int WM, bool GATEUP, bool W8, int BK = kBK, int NS = 2,
+          bool SPLIT = false>
 __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs a, int n_mt,
-                                                                    int n_nt) {
+                                                                    int n_nt, int nsplit,
+                                                                    int per, float* ws) {
   constexpr int NW = WN * WM;
   constexpr int CPR = BK / 8;
   constexpr int RPI = 1024 / (BK * 2);
@@ -410,7 +415,9 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   constexpr int CPRO = TNO / 8;               // 16-byte chunks per strip row
   static_assert(BK == 64 || (BK == 128 && WN * WM == 4 && !W8),
                 "32-wide k-substeps: two per k-step, or four with four bf16 waves");
-  static_assert(NS == 2 || (NS == 3 && WN * WM == 4 && !W8), "three LDS stages: four bf16 waves");
+  static_assert(NS == 2 || ((NS == 3 || NS == 4) && WN * WM == 4 && !W8),
+                "three or four LDS stages: four bf16 waves");
+  static_assert(!SPLIT || NS > 2, "k split across workgroups: the staged four-wave loop");
   static_assert(BN % WRPI == 0 && BM % (RPI * NW) == 0, "tile/waves");
   static_assert(W8 || NWI % NW == 0, "bf16 weight loads spread evenly over the waves");
   static_assert(NQC % kWave == 0, "int8 chunks: whole waves");
@@ -423,9 +430,11 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   __shared__ __attribute__((aligned(1024))) uint16_t sW0[BN][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sW1[BN][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sW2[NS > 2 ? BN : 1][BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sW3[NS > 3 ? BN : 1][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX0[BM][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX1[BM][BK];
   __shared__ __attribute__((aligned(1024))) uint16_t sX2[NS > 2 ? BM : 1][BK];
+  __shared__ __attribute__((aligned(1024))) uint16_t sX3[NS > 3 ? BM : 1][BK];
   __shared__ __attribute__((aligned(1024))) uint8_t sQ0[W8 ? BN : 1][BK];
   __shared__ __attribute__((aligned(1024))) uint8_t sQ1[W8 ? BN : 1][BK];
 
@@ -435,7 +444,9 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   const int li = lane & 15, grp = lane >> 4;
 
   // this workgroup's tiles: XCD xcd owns tiles [T xcd / 8, T (xcd + 1) / 8)
-  const int T = n_mt * n_nt;
+  // (SPLIT: work items (k range, tile), the k range slowest)
+  const int TT = n_mt * n_nt;
+  const int T = TT * (SPLIT ? nsplit : 1);
   const int xcd = (int)blockIdx.x % 8, gx = (int)gridDim.x / 8;
   const int t_end = (int)((int64_t)T * (xcd + 1) / 8);
   int b = (int)((int64_t)T * xcd / 8) + (int)blockIdx.x / 8;
@@ -447,14 +458,23 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
   void* const wptr1 = (void*)(GATEUP ? a.w1 : a.w0);
   const int lrow = lane / CPR, lchunk = lane % CPR;
 
-  // per-tile state: origin, DMA lane offsets and (int8) the scales of the
-  // rows this lane dequantises
-  int64_t m0 = 0, c0 = 0;
+  // per-tile state: origin, k range (SPLIT: k-steps kb .. kb + nloc - 1;
+  // else all nkt), DMA lane offsets and (int8) the scales of the rows this
+  // lane dequantises
+  const int64_t nkt = a.K / BK;
+  int64_t m0 = 0, c0 = 0, kb = 0, nloc = nkt;
+  int ks = 0;
   uint32_t woff[IW], xoff[IX];
   float qs[W8 ? QCH : 1], qn[W8 ? QCH : 1];
   auto wrow_n = [&](int t) -> int64_t { return GATEUP ? c0 + (t / 32) * 16 + (t % 16) : c0 + t; };
   auto wrow_up = [&](int t) -> bool { return GATEUP && ((t / 16) & 1); };
   auto setup = [&](int bb) {
+    if constexpr (SPLIT) {
+      ks = bb / TT;
+      bb -= ks * TT;
+      kb = (int64_t)ks * per;
+      nloc = nkt - kb < per ? nkt - kb : per;
+    }
     const int gbase = (bb / (kGroupM * n_nt)) * kGroupM;
     const int gm = n_mt - gbase < kGroupM ? n_mt - gbase : kGroupM;
     const int gin = bb - gbase * n_nt;
@@ -496,14 +516,15 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
       if (NWI % NW != 0 && q >= NWI) break;  // uniform per wave
       const bool up = wrow_up(q * WRPI);
       load_lds16(up ? wptr1 : a.w0, live ? (up ? wbytes1 : wbytes0) : 0,
-                 (lds_ptr_t)((char*)dst + q * WRPI * BK * WB), woff[j], (uint32_t)(k0 * WB));
+                 (lds_ptr_t)((char*)dst + q * WRPI * BK * WB), woff[j],
+                 (uint32_t)((kb * BK + k0) * WB));
     }
   };
   auto issue_x = [&](uint16_t (*tx)[BK], int64_t k0, bool live = true) {
 #pragma unroll
     for (int j = 0; j < IX; ++j)
       load_lds16(a.x, live ? xbytes : 0, (lds_ptr_t)&tx[(wave + NW * j) * RPI][0], xoff[j],
-                 (uint32_t)(k0 * 2));
+                 (uint32_t)((kb * BK + k0) * 2));
   };
   // int8: chunk c of this lane (16 weights of row r, k-range 16 q .. 16 q +
   // 15 of the step) from staging buffer sq to bf16(q * s) in stage tw, in
@@ -607,12 +628,15 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     if constexpr (NW >= 8) __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto stw = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sW0 : (st == 1 ? sW1 : sW2); };
-  auto stx = [&](int st) -> uint16_t (*)[BK] { return st == 0 ? sX0 : (st == 1 ? sX1 : sX2); };
+  auto stw = [&](int st) -> uint16_t (*)[BK] {
+    return st == 0 ? sW0 : (st == 1 ? sW1 : (st == 2 ? sW2 : sW3));
+  };
+  auto stx = [&](int st) -> uint16_t (*)[BK] {
+    return st == 0 ? sX0 : (st == 1 ? sX1 : (st == 2 ? sX2 : sX3));
+  };
   auto stq = [&](int st) -> uint8_t (*)[BK] { return st == 0 ? sQ0 : sQ1; };
   // a tile's first loads: k-step 0 into stage 0 (int8: the weights of steps
   // 0 and 1 into the staging buffers)
-  const int64_t nkt = a.K / BK;
   auto issue_first = [&]() {
     issue_x(sX0, 0);
     if constexpr (W8) {
@@ -663,16 +687,20 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
         __syncthreads();
         if (nkt > 2) issue_w(sQ0, 2 * BK);
         if (nkt > 1) issue_x(sX1, BK);
+      } else if constexpr (NS > 2) {
+        // steps 1 .. NS - 1 into their stages (past the last step: empty
+        // ranges, so that every step has issued the same loads)
+#pragma unroll
+        for (int st = 1; st < NS; ++st) {
+          const bool live = st < nloc;
+          issue_x(stx(st), live ? st * BK : 0, live);
+          issue_w(stw(st), live ? st * BK : 0, live);
+        }
       } else {
         if (nkt > 1) {
           issue_x(sX1, BK);
           issue_w(sW1, BK);
         }
-        if constexpr (NS > 2)
-          if (nkt > 2) {
-            issue_x(sX2, 2 * BK);
-            issue_w(sW2, 2 * BK);
-          }
       }
 #pragma unroll
       for (int j = 0; j < FM; ++j) rd_b(F, sX0, 0, j);
@@ -691,20 +719,22 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
       // double-buffers the accumulators and spills.)
       if constexpr (NW == 4) {
         // the same steps for an even nkt (the launcher checks), without the
-        // odd-count exit. With three stages (NS = 3) step k lives in stage
-        // k % 3, the loads of step k + 3 go out after step k's barrier, and
-        // the wait before that barrier leaves step k + 2's loads in flight
-        // (LPS per wave): loads get two steps to land instead of one. Every
-        // step issues its loads, past the last step with an empty range, so
-        // that the compiler's count of loads in flight is exact (it would
+        // odd-count exit. With NS = 3 or 4 stages step k lives in stage
+        // k % NS, the loads of step k + NS go out after step k's barrier,
+        // and the wait before that barrier leaves the loads of steps k + 2
+        // .. k + NS - 1 in flight (LPS per wave and step): loads get NS - 1
+        // steps to land instead of one. Every step issues its loads, past
+        // the last step with an empty range, so that the count of loads in
+        // flight is exact, for that wait and for the compiler (which would
         // otherwise wait for all of them before the next stage's reads).
         constexpr int LPS = IW + IX;  // load instructions per wave and k-step
-        for (int64_t kt = 0; kt < nkt; kt += NS) {
+        static_assert((NS - 2) * LPS < 64, "loads in flight within the vmcnt range");
+        for (int64_t kt = 0; kt < nloc; kt += NS) {
 #pragma unroll
           for (int u = 0; u < NS; ++u) {
             const int64_t k = kt + u;
             if constexpr (NS > 2)
-              if (k >= nkt) break;
+              if (k >= nloc) break;
             mma(std::true_type{}, std::false_type{}, F, G, stw(u), stx(u), 1, sQ0, sW0);
             if constexpr (BK == 128) {
               // substeps 1 and 2 of the four, each reading the next
@@ -715,20 +745,17 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
               // this wave's loads of step k + 1 have landed and its reads of
               // stage u are done; then a bare barrier (__syncthreads' fence
               // would wait for every load in flight)
-              if (k + 2 < nkt)
-                __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(LPS));
-              else
-                __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));
+              __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm((NS - 2) * LPS));
               __builtin_amdgcn_s_barrier();
             } else {
               __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
               __syncthreads();
             }
             if constexpr (NS > 2) {
-              const bool live = k + NS < nkt;
+              const bool live = k + NS < nloc;
               issue_x(stx(u), live ? (k + NS) * BK : 0, live);
               issue_w(stw(u), live ? (k + NS) * BK : 0, live);
-            } else if (k + NS < nkt) {
+            } else if (k + NS < nloc) {
               issue_x(stx(u), (k + NS) * BK);
               issue_w(stw(u), (k + NS) * BK);
             }
@@ -794,9 +821,45 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
     const int bnext = b + gx;
     const bool more = bnext < t_end;
     const int64_t em0 = m0, ec0 = c0;
+    const int eks = ks;
     if (more) {
       setup(bnext);
       issue_first();
+    }
+    if constexpr (SPLIT) {
+      // fp32 partials of k range eks into ws[eks][m][col] (col: output
+      // column n; gate-up: g at n, u at N + n), 4 consecutive columns of one
+      // x row per lane, for splitk_reduce_kernel
+      const int64_t wc = GATEUP ? 2 * a.N : a.N;
+      const bool v16 = (wc & 3) == 0;
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int64_t m = em0 + wm * TM + j * 16 + li;
+        if (m >= a.M) continue;
+        float* prow = ws + ((int64_t)eks * a.M + m) * wc;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+          int64_t n, col;
+          if constexpr (GATEUP) {
+            const int sub = (wn * TN) / 16 + i;  // even: gate rows, odd: up rows
+            n = ec0 + (sub / 2) * 16 + 4 * grp;
+            col = (sub & 1) ? a.N + n : n;
+          } else {
+            n = ec0 + wn * TN + i * 16 + 4 * grp;
+            col = n;
+          }
+          if (v16 && n + 3 < a.N) {
+            *reinterpret_cast<f32x4*>(prow + col) = acc[i][j];
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n + r < a.N) prow[col + r] = acc[i][j][r];
+          }
+        }
+      }
+      if (!more) break;
+      b = bnext;
+      continue;
     }
     // ---- epilogue: per wave, 16 x rows at a time through its strip ----
     uint16_t* strip = &sX1[0][0] + wave * 16 * SROW;
@@ -911,7 +974,28 @@ int launch_tiles_cfg(const StreamArgs& a, hipStream_t s) {
   const int64_t tiles = (int64_t)n_nt * n_mt;
   const int grid = tiles < kTilesGrid ? (int)((tiles + 7) / 8 * 8) : kTilesGrid;
   hipLaunchKernelGGL((gemm_tiles_kernel<BN, BM, WN, WM, GATEUP, W8, BK, NS>), dim3((unsigned)grid),
-                     dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt);
+                     dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt, 1, 0, (float*)nullptr);
+  return (int)hipGetLastError();
+}
+
+// The staged four-wave tiles with k split across workgroups: `used` ranges
+// of `per` 128-wide k-steps (the last may be shorter, none empty), fp32
+// partials in ws (used planes of M x N, gate-up M x 2N), then the reduce.
+template <int BN, int BM, int WN, int WM, bool GATEUP, int NS>
+int launch_tiles_split_cfg(const StreamArgs& a, int used, int per, float* ws, hipStream_t s) {
+  const int64_t cols = GATEUP ? BN / 2 : BN;
+  const int n_nt = (int)((a.N + cols - 1) / cols);
+  const int n_mt = (int)((a.M + BM - 1) / BM);
+  const int64_t items = (int64_t)n_nt * n_mt * used;
+  const int grid = items < kTilesGrid ? (int)((items + 7) / 8 * 8) : kTilesGrid;
+  hipLaunchKernelGGL((gemm_tiles_kernel<BN, BM, WN, WM, GATEUP, false, 2 * kBK, NS, true>),
+                     dim3((unsigned)grid), dim3(WN * WM * kWave), 0, s, a, n_mt, n_nt, used, per,
+                     ws);
+  int e = (int)hipGetLastError();
+  if (e) return e;
+  const int64_t threads = a.M * ((a.N + 3) / 4);
+  hipLaunchKernelGGL(splitk_reduce_kernel<GATEUP>, dim3((unsigned)((threads + 255) / 256)),
+                     dim3(256), 0, s, ws, used, a);
   return (int)hipGetLastError();
 }
 
@@ -1364,12 +1448,31 @@ GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
 
 int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K, bool gateup) {
   if (p.tile < 0) return 0;
+  if (p.tile == kT96x64) return (int64_t)p.nsplit * M * (gateup ? 2 * N : N);
   return (int64_t)gemm_splitk_used(K, p.nsplit) * M * (gateup ? 2 * N : N);
 }
 
 GemmSplit gemm_split_plan_bf16(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (small_round_tile(M, N, K, gateup) >= 0) return GemmSplit{-1, 1};
-  return gemm_split_plan(M, N, K, gateup);
+  const GemmSplit p = gemm_split_plan(M, N, K, gateup);
+  if (p.tile < 0 || M <= 64 || K % (2 * kBK) != 0) return p;
+  // The staged 96 x 64 four-wave tiles (three LDS stages), k split into
+  // ranges of 4 to 32 128-wide steps, as many as one round of at most 256
+  // work items allows; ranges above 8 steps only with at least 192 items.
+  // Measured on MI355X against the split above (gemm_kernel, 64-wide steps;
+  // µs): 8B TP=4 QKV 4096 -> 1536 at M = 256 21.1 -> 17.5, 8B TP=8 QKV
+  // 4096 -> 768 at 512 19.8 -> 16.1, 4B o 4096 -> 2560 at 136 22.1 -> 17.7,
+  // 4B down 9728 -> 2560 at 128 30.7 -> 25.6, 0.6B down 3072 -> 1024 at 384
+  // 17.5 -> 15.0; with 172-176 items over 12-16 steps (8B o at 96-128 rows,
+  // 0.6B down at 512) 4-8% slower, with two rounds of items up to 1.8x.
+  const int64_t nk = K / (2 * kBK), n = tile_count(kT96x64, M, N, gateup);
+  int64_t ns = kCUs / n;
+  ns = ns < 16 ? ns : 16;
+  ns = ns < nk / 4 ? ns : nk / 4;
+  if (ns < 2) return p;
+  const int64_t per = (nk + ns - 1) / ns;
+  if (per > 32 || (per > 8 && n * ns < 192)) return p;
+  return GemmSplit{kT96x64, (int)((nk + per - 1) / per)};
 }
 
 bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p) {
@@ -1380,6 +1483,16 @@ bool use_gemm_split(const StreamArgs& a, bool aligned, bool gateup, GemmSplit* p
 
 template <bool GATEUP, bool W8>
 int launch_gemm_split(const StreamArgs& a, const GemmSplit& p, hipStream_t s) {
+  if constexpr (!W8) {
+    if (p.tile == kT96x64) {
+      // nsplit ranges of per 128-wide k-steps (gemm_split_plan_bf16)
+      const int64_t nk = a.K / (2 * kBK);
+      const int per = (int)((nk + p.nsplit - 1) / p.nsplit);
+      if (a.K % (2 * kBK) != 0 || (nk + per - 1) / per != p.nsplit) return (int)hipErrorInvalidValue;
+      if constexpr (GATEUP) return launch_tiles_split_cfg<96, 64, 1, 4, true, 3>(a, p.nsplit, per, a.ws, s);
+      return launch_tiles_split_cfg<96, 64, 2, 2, false, 3>(a, p.nsplit, per, a.ws, s);
+    }
+  }
   switch (p.tile) {
     case kT64x32: return launch_gemm_splitk_cfg<64, 32, 2, 2, GATEUP, 3, W8>(a, p.nsplit, a.ws, s);
     case kT128x64: return launch_gemm_splitk_cfg<128, 64, 4, 2, GATEUP, 2, W8>(a, p.nsplit, a.ws, s);
