@@ -1455,7 +1455,7 @@ int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K
 GemmSplit gemm_split_plan_bf16(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (small_round_tile(M, N, K, gateup) >= 0) return GemmSplit{-1, 1};
   const GemmSplit p = gemm_split_plan(M, N, K, gateup);
-  if (p.tile < 0 || M <= 64 || K % (2 * kBK) != 0) return p;
+  if (p.tile < 0 || K % (2 * kBK) != 0) return p;
   // The staged 96 x 64 four-wave tiles (three LDS stages), k split into
   // ranges of 4 to 32 128-wide steps, as many as one round of at most 256
   // work items allows; ranges above 8 steps only with at least 192 items.
@@ -1463,8 +1463,9 @@ GemmSplit gemm_split_plan_bf16(int64_t M, int64_t N, int64_t K, bool gateup) {
   // µs): 8B TP=4 QKV 4096 -> 1536 at M = 256 21.1 -> 17.5, 8B TP=8 QKV
   // 4096 -> 768 at 512 19.8 -> 16.1, 4B o 4096 -> 2560 at 136 22.1 -> 17.7,
   // 4B down 9728 -> 2560 at 128 30.7 -> 25.6, 0.6B down 3072 -> 1024 at 384
-  // 17.5 -> 15.0; with 172-176 items over 12-16 steps (8B o at 96-128 rows,
-  // 0.6B down at 512) 4-8% slower, with two rounds of items up to 1.8x.
+  // 17.5 -> 15.0, 4B down at 64 23.9 -> 20.1, 8B QKV 4096 -> 6144 at 64 20.7
+  // -> 18.8; with 172-176 items over 12-16 steps (8B o at 96-128 rows, 0.6B
+  // down at 512) 4-8% slower, with two rounds of items up to 1.8x.
   const int64_t nk = K / (2 * kBK), n = tile_count(kT96x64, M, N, gateup);
   int64_t ns = kCUs / n;
   ns = ns < 16 ? ns : 16;

@@ -138,10 +138,10 @@ struct GemmSplit {
 };
 GemmSplit gemm_split_plan(int64_t M, int64_t N, int64_t K, bool gateup);
 // The split of a bf16 call: none where a round of small three-stage tiles
-// (small_round_tile) runs instead; above 64 rows with 128-wide k-steps
-// mostly the staged 96 x 64 four-wave tiles (tile kT96x64 of fp_gemm.hip,
-// nsplit ranges of 128-wide k-steps). int8 calls that split on their int8
-// weights keep gemm_split_plan.
+// (small_round_tile) runs instead; with 128-wide k-steps mostly the staged
+// 96 x 64 four-wave tiles (tile kT96x64 of fp_gemm.hip, nsplit ranges of
+// 128-wide k-steps). int8 calls that split on their int8 weights keep
+// gemm_split_plan.
 GemmSplit gemm_split_plan_bf16(int64_t M, int64_t N, int64_t K, bool gateup);
 int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K, bool gateup);
 // Whether the bf16 call a runs split (plan + workspace large enough).

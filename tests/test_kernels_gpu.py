@@ -715,8 +715,8 @@ def test_wide_k_and_320_tiles_ragged(op, M, K, N):
 def test_split_k_across_workgroups(M, N, K, op):
     """Calls the planner splits across workgroups (fp32 partials in a torch
     workspace, fixed-order reduce): narrow and ragged N (scalar partial
-    stores), ragged M, every split tile (above 64 rows with 128-wide steps:
-    the staged 96 x 64 four-wave tiles); repeated calls are bit-identical."""
+    stores), ragged M, every split tile (with 128-wide steps mostly the
+    staged 96 x 64 four-wave tiles); repeated calls are bit-identical."""
     from llms_amd import _lib
 
     assert _lib.capi().fp_workspace_bytes(M, N, K, int(op == "gate-up")) > 0
