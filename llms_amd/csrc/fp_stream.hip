@@ -358,6 +358,10 @@ int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
   // workgroups (fp_gemm.hip)
   GemmSplit sp;
   if (!W8 && use_gemm_split(a, aligned, GATEUP, &sp)) return launch_gemm_split<GATEUP, false>(a, sp, s);
+  // bf16 with a nearly full round of small staged tiles (from 48 rows
+  // against large weights): fp_gemm.hip
+  if (!W8 && small_round_tile(a.M, a.N, a.K, GATEUP) >= 0 && gemm_supported(a, aligned, false))
+    return launch_gemm<GATEUP, false>(a, s);
   // bf16 from 3 (small N, e.g. QKV) or 8 rows: split-K tiles (fp_splitk.hip)
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
   const int64_t min_m = wrows <= kSplitkSmallN ? kSplitkMinMSmallN : kSplitkMinM;

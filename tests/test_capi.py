@@ -51,15 +51,14 @@ def test_library_exports_every_declared_symbol():
 def test_workspace_bytes_plan():
     """The split-k plan (a host function: no GPU needed). Splits only where
     the unsplit grid leaves the chip idle and k is long: Qwen3 down from 32
-    rows, o at 256 rows, 8B QKV at 128, 8B TP=8 QKV shards (768 columns) at
-    512;
-    never for short K, few rows, K % 64 != 0, a chip-filling grid, where one
-    round of tiles with 128-wide k-steps runs instead with at most 6 splits
-    (4B QKV at 256 rows, 4B o at 640) or 3 (8B o at 1024), or where a round
-    of small three-stage tiles with enough tiles per k-step runs instead (8B
-    QKV at 256 rows, 4B TP=4 QKV shards at 512). The workspace
-    holds one fp32 plane per k range, 2..16 ranges, of M x N (gate-up: M x
-    2N)."""
+    rows, o at 256 rows, 8B QKV at 128, 8B gate-up at 40, 8B TP=8 QKV shards
+    (768 columns) at 512; never for short K, few rows, K % 64 != 0, a
+    chip-filling grid, where one round of tiles with 128-wide k-steps runs
+    instead with at most 6 splits (4B QKV at 256 rows, 4B o at 640) or 3 (8B
+    o at 1024), or where a round of small three-stage tiles with enough tiles
+    per k-step runs instead (8B QKV at 256 rows, 8B gate-up at 64, 4B TP=4
+    QKV shards at 512). The workspace holds one fp32 plane per k range,
+    2..16 ranges, of M x N (gate-up: M x 2N)."""
     from llms_amd import _lib
 
     wb = _lib.capi().fp_workspace_bytes
@@ -79,7 +78,7 @@ def test_workspace_bytes_plan():
     assert 2 <= planes(512, 768, 4096) <= 16                # 8B TP=8 QKV: 64 tiles, 32 k-steps
     assert 2 <= planes(128, 1024, 3072) <= 16               # 0.6B down, few tiles
     assert 2 <= planes(300, 1001, 8192) <= 16                # narrow, ragged N
-    assert 2 <= planes(64, 12288, 4096, 1) <= 16             # 8B gate-up, 64 rows
+    assert 2 <= planes(40, 12288, 4096, 1) <= 16             # 8B gate-up, 40 rows
     assert 2 <= planes(200, 1001, 8192, 1) <= 16             # gate-up, ragged N
     for args in [(16, 2560, 9728, 0), (31, 2560, 9728, 0), (512, 6144, 2560, 0),
                  (2048, 9728, 2560, 1), (256, 4096, 1024, 0), (64, 2560, 4096, 0),
@@ -87,7 +86,7 @@ def test_workspace_bytes_plan():
                  (512, 0, 9728, 0), (64, 9728, 2560, 1), (32, 12288, 4096, 1),
                  (128, 9728, 2560, 1), (32, 6144, 4096, 0), (256, 6144, 2560, 0),
                  (640, 2560, 4096, 0), (1024, 4096, 4096, 0), (256, 6144, 4096, 0),
-                 (512, 1536, 2560, 0)]:
+                 (512, 1536, 2560, 0), (64, 12288, 4096, 1)]:
         assert wb(*args) == 0, args
     # ranges hold at least 8 k-steps of 64
     assert planes(32, 2560, 2048) <= 4
