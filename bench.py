@@ -501,7 +501,7 @@ PROFILE_SET = [
     ("int8 prefill", "qwen3-4b", 2048, True, 1),
     ("bf16 verify M=3", "qwen3-4b", 3, False, 1),
     ("bf16 verify M=8", "qwen3-4b", 8, False, 1),
-    ("split-K tiles M=64", "qwen3-8b", 64, False, 1),
+    ("8B M=64", "qwen3-8b", 64, False, 1),
     ("8B M=256", "qwen3-8b", 256, False, 1),
     ("prefill M=8192", "qwen3-4b", 8192, False, 1),
     ("8B TP=2 shard M=512", "qwen3-8b", 512, False, 2),
