@@ -277,7 +277,9 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
   if constexpr (SPLIT) {
     // fp32 partials: 4 consecutive columns of one x row per lane
     const int64_t wc = GATEUP ? 2 * a.N : a.N;
-    const bool v16 = (wc & 3) == 0;
+    // 16-byte partial stores where every column offset is a multiple of 4
+    // (gate-up: u at N + n, so N itself must be)
+    const bool v16 = (a.N & 3) == 0;
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int64_t m = m0 + wm * TM + j * 16 + li;
@@ -831,7 +833,7 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_tiles_kernel(StreamArgs 
       // column n; gate-up: g at n, u at N + n), 4 consecutive columns of one
       // x row per lane, for splitk_reduce_kernel
       const int64_t wc = GATEUP ? 2 * a.N : a.N;
-      const bool v16 = (wc & 3) == 0;
+      const bool v16 = (a.N & 3) == 0;  // as in gemm_kernel's split form
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
         const int64_t m = em0 + wm * TM + j * 16 + li;
@@ -920,7 +922,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int
   const int64_t plane = a.M * wc;  // floats per split
   const float* p = ws + m * wc + n;
   uint32_t h[4];
-  if ((wc & 3) == 0 && n + 3 < a.N) {
+  if ((a.N & 3) == 0 && n + 3 < a.N) {  // 16-byte partials (u at N + n)
     f32x4 g = *reinterpret_cast<const f32x4*>(p);
     f32x4 u = GATEUP ? *reinterpret_cast<const f32x4*>(p + a.N) : f32x4{};
     for (int s = 1; s < nsplit; ++s) {

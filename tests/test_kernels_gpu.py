@@ -711,7 +711,8 @@ def test_wide_k_and_320_tiles_ragged(op, M, K, N):
     (32, 2560, 9728, "linear"), (100, 4096, 12288, "linear"), (300, 1001, 8192, "linear"),
     (1024, 2560, 9728, "linear"), (2048, 2560, 9728, "linear"), (128, 6144, 4096, "qkv"),
     (40, 12288, 4096, "gate-up"), (200, 1001, 8192, "gate-up"), (77, 4096, 4096, "linear"),
-    (512, 768, 4096, "qkv"), (136, 3072, 4096, "qkv"), (150, 1000, 8192, "gate-up")])
+    (512, 768, 4096, "qkv"), (136, 3072, 4096, "qkv"), (150, 1000, 8192, "gate-up"),
+    (150, 1002, 8192, "gate-up"), (40, 1002, 12288, "gate-up")])
 def test_split_k_across_workgroups(M, N, K, op):
     """Calls the planner splits across workgroups (fp32 partials in a torch
     workspace, fixed-order reduce): narrow and ragged N (scalar partial
