@@ -78,7 +78,9 @@ def fused_gate_up_silu_w8(
       187 against 203 us, because the in-register tiles cannot use the
       320 x 256 tile.
 
-    Every form gives the same result as the dequantise-then-matmul path."""
+    Every form computes the bf16 contract on bf16(q * s), the
+    dequantise-then-matmul result up to the fp32 summation order of the plan
+    that runs."""
     if qg.shape != qu.shape:
         raise ValueError(f"qg shape {tuple(qg.shape)} != qu shape {tuple(qu.shape)}")
     if qg.dim() != 2:
