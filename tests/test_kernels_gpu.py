@@ -334,16 +334,18 @@ def test_prefill_rows_independent_of_grid_plan(kind):
 
 
 @pytest.mark.parametrize("M,K,N", [
-    (512, 2560, 9728),    # Qwen3-4B: 192 x 256 tiles with four waves
+    (512, 2560, 9728),    # Qwen3-4B: one round of 160 x 256 four-wave tiles
     (500, 2560, 9700),    # the same, partial tiles in M and N
-    (512, 4096, 12288),   # Qwen3-8B: four waves, 64 k-steps
+    (512, 4096, 12288),   # Qwen3-8B: 192 x 256 tiles with four waves, 64 k-steps
+    (500, 4096, 12200),   # the same, partial tiles in M and N
     (2048, 1024, 3072),   # Qwen3-0.6B, 16 k-steps: eight waves
-    (512, 2496, 9728)])   # 39 k-steps (odd): eight waves
+    (512, 2496, 9728)])   # 39 k-steps (odd): 192 x 256 with eight waves
 def test_gate_up_four_wave_tiles(M, K, N):
     """bf16 gate-up calls planned on 192 x 256 tiles run four waves per
     workgroup (accumulators in AGPRs) when the k-step count is even and at
-    least 32, else eight: both against the oracle, and repeated calls
-    bit-identical (the tile order and the k order do not depend on timing)."""
+    least 32, else eight, and a round of 160 x 256 tiles four: all against
+    the oracle, and repeated calls bit-identical (the tile order and the k
+    order do not depend on timing)."""
     x, wg, wu = ffn_inputs(230 + M, M, K, N)
     xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
     y = _kernels().triton_fused_gate_up_silu(xd, wgd, wud).cpu()
@@ -388,6 +390,7 @@ def test_192x128_four_wave_tiles(case):
     ("gate-up", 2048, 1500, 2560, 1216),  # 128 x 160 tiles; 1500 rows: 128 x 128
     ("gate-up", 2000, 1500, 2560, 1216),  # 128 x 160, partial last m-tile
     ("gate-up", 512, 1024, 2560, 4864),   # 160 x 128 (one wave column); 1024 rows: 192 x 256
+    ("gate-up", 512, 1024, 2560, 9728),   # 160 x 256, 64-wide steps; 1024 rows: 320 x 256
     ("qkv", 1024, 768, 2560, 5000),       # 160 x 128; 768 rows: 128 x 128
     ("qkv", 2048, 1024, 2560, 2432)])     # 128 x 160; 1024 rows: 128 x 128
 def test_four_wave_128_wide_steps(op, M, M2, K, N):
