@@ -1199,11 +1199,12 @@ bool k128_wide(int64_t M, int64_t N, int64_t K, bool gateup) {
 
 // A single round of small four-wave tiles with three LDS stages (bf16,
 // 128-wide k-steps, at least 48 rows): 96 x 64 where at most 256 of them
-// cover the output, else 64 x 128 with 192-256 tiles, either with enough
-// tiles against the k loop: 3 per k-step for gate-up and for up to 24
-// k-steps, 6 per k-step above, and up to 128 rows at least 192 tiles (fewer
-// leave the call to k split across or inside workgroups, or to the
-// weight-streaming kernels); -1 if neither. The third stage gives each k-step's
+// cover the output, else 64 x 128 with 192-256 tiles (above 512 rows 240-256
+// and at least 24 k-steps), either with enough tiles against the k loop: 3
+// per k-step for gate-up and for up to 24 k-steps, 6 per k-step above; at
+// least 64, 128 with up to 12 k-steps, and up to 128 rows at least 192
+// (fewer leave the call to k split across or inside workgroups, to the
+// weight-streaming kernels, or to two 64 x 64 tiles per CU); -1 if neither. The third stage gives each k-step's
 // loads two steps to land instead of one, and the small tiles keep three
 // stages within the LDS (120 and 144 KB). Measured on MI355X over Qwen3
 // 0.6B/4B/8B QKV, gate-up, o, down and their tensor-parallel (TP) shards at
@@ -1217,8 +1218,12 @@ bool k128_wide(int64_t M, int64_t N, int64_t K, bool gateup) {
 // o 4096 -> 4096 at 512 (64 x 128) 32.7 -> 27.9; at 48-128 rows 4B gate-up
 // 2560 -> 2 x 9728 at 64 39.4 -> 28.8, 8B gate-up 4096 -> 2 x 12288 at 64
 // 50.5 -> 43.9, 8B TP=2 gate-up 4096 -> 2 x 6144 at 128 56.7 -> 34.9 (with
-// 64-128 tiles there, or fewer than 48 rows, up to 2x slower). With 32
-// k-steps and 96-129
+// 64-128 tiles there, or fewer than 48 rows, up to 2x slower). Over 44
+// random shapes (M = 48-4096, K = 1024-8192) against the plans before these
+// tiles: 8 faster by 10-35%, and the ones slower by 7-13% (few tiles against
+// 8-12 k-steps: linear 1024 -> 776 at 768 rows 8.6 -> 9.4 us, QKV 1536 ->
+// 1024 at 1536 rows 11.7 -> 13.3 us; 64 x 128 with 204 tiles above 512 rows)
+// set the minimum counts above. With 32 k-steps and 96-129
 // tiles the split plans were 4-12% faster (8B TP=2 QKV at 192 rows 22.4 vs
 // 25.1, 8B o at 192 23.6 vs 25.4), with 76 k-steps 13% (4B down at 768). The
 // same tiles with two stages: 96 x 64 on 8B TP=2 QKV at 512 32.2, 64 x 128
@@ -1227,11 +1232,14 @@ int small_round_tile(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (K % (2 * kBK) != 0 || M < 48) return -1;
   const int64_t nk = K / (2 * kBK);
   int64_t need = (gateup || nk <= 24 ? 3 : 6) * nk;
+  if (need < 64) need = 64;
+  if (nk <= 12 && need < 128) need = 128;
   if (M <= 128 && need < 192) need = 192;
   const int64_t n1 = tile_count(kT96x64, M, N, gateup);
   if (n1 <= kCUs) return n1 >= need ? kT96x64 : -1;
   const int64_t n2 = tile_count(kT64x128w, M, N, gateup);
-  return n2 >= 192 && n2 <= kCUs && n2 >= need ? kT64x128w : -1;
+  if (n2 > kCUs || n2 < need) return -1;
+  return (M <= 512 ? n2 >= 192 : n2 >= 240 && nk >= 24) ? kT64x128w : -1;
 }
 
 GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf16) {
