@@ -1261,9 +1261,12 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf
   GemmPlan best{kT64x128, 0};
   double cbest = grid_cost(kT64x128, M, N, nkt, gateup);
   for (int t : {kT128x128, kT256x256, kT192x256, kT320x256}) {
-    // 320 x 256 (bf16 only) for at most two rounds: beyond, the model
-    // underrates it by 2-4%
-    if (t == kT320x256 && (!bf16 || tile_count(t, M, N, gateup) > 2 * kCUs)) continue;
+    // 320 x 256 (bf16 only); QKV-like outputs for at most two rounds: beyond,
+    // the model underrates it (4B QKV M = 8192 226 against 206 us on 256 x
+    // 256). Gate-up at any count (same-box A/B against 256 x 256 and its
+    // tail, 4B gate-up: M = 3072 260 -> 248 us, 4096 345 -> 332, 6144 509 ->
+    // 483, 8192 668 -> 651).
+    if (t == kT320x256 && (!bf16 || (!gateup && tile_count(t, M, N, gateup) > 2 * kCUs))) continue;
     const double c = grid_cost(t, M, N, nkt, gateup);
     if (c < cbest) best = GemmPlan{t, 0}, cbest = c;
   }
