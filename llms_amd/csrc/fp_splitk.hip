@@ -64,8 +64,11 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
   static_assert(BN % 16 == 0 && BM % 16 == 0 && BN % WRPI == 0, "tile");
   static_assert(!GATEUP || BN % 32 == 0, "gate-up tiles hold whole gate/up 16-row pairs");
   static_assert(NS == 2 || NS == 3, "LDS stages");
-  // the partial tiles of waves 1 .. NW-1 are summed in stage 0's space
-  static_assert((NW - 1) * FN * FM * 256 * 4 <= NW * (SW + SX), "reduction space");
+  // the partial tiles of waves 1 .. NW-1 are summed in stage 0's space, FC
+  // weight fragments (all FM x fragments of each) per pass
+  constexpr int FC0 = NW * (SW + SX) / ((NW - 1) * FM * 1024);
+  constexpr int FC = FC0 >= FN ? FN : FC0;
+  static_assert(FC >= 1, "reduction space");
 
   // One LDS object per stage (distinct alias scopes: reads of one stage are
   // not ordered after the asynchronous writes into another), each split per
@@ -199,24 +202,33 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
     }
   }
 
-  // Fixed-order cross-wave sum through LDS (the ring is free now).
+  // Fixed-order cross-wave sum through LDS (the ring is free now), in passes
+  // of FC weight fragments where the partials of a large tile do not fit
+  // one stage: each output is still summed in wave order 0, 1, ..., NW - 1.
   float* red = reinterpret_cast<float*>(&sS0[0][0]);
-  __syncthreads();
-  if (wave > 0) {
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+  for (int p0 = 0; p0 < FN; p0 += FC) {
+    __syncthreads();
+    if (wave > 0) {
 #pragma unroll
-      for (int j = 0; j < FM; ++j)
-        *reinterpret_cast<f32x4*>(red + (((wave - 1) * FN + i) * FM + j) * 256 + lane * 4) = acc[i][j];
+      for (int i = p0; i < p0 + FC && i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          *reinterpret_cast<f32x4*>(red + (((wave - 1) * FC + i - p0) * FM + j) * 256 + lane * 4) =
+              acc[i][j];
+    }
+    __syncthreads();
+    if (wave == 0) {
+      for (int w = 0; w < NW - 1; ++w)
+#pragma unroll
+        for (int i = p0; i < p0 + FC && i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
+            acc[i][j] += *reinterpret_cast<const f32x4*>(
+                red + ((w * FC + i - p0) * FM + j) * 256 + lane * 4);
+    }
   }
-  __syncthreads();
   if (wave != 0) return;
-  for (int w = 0; w < NW - 1; ++w)
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-        acc[i][j] += *reinterpret_cast<const f32x4*>(red + ((w * FN + i) * FM + j) * 256 + lane * 4);
 
   // Epilogue: D lane holds rows 4*grp + r (weight rows) of column li (x row).
   const bool y8 = ((a.ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 7) == 0);
@@ -285,9 +297,26 @@ bool splitk_supported(const StreamArgs& a, bool aligned, bool w8) {
 // 10.7-11.2 -> 8.8-9.6; 4B QKV 768 and 1536 columns 6.0-6.8 -> 4.6-5.9;
 // 0.6B down (1024 x 3072) 6.5-7.0 -> 5.7-6.3. The full Qwen3-4B/8B outputs
 // keep 4 waves (8 were 2-14% slower there).
+// int8 gate-up over wide outputs (at least 7680 columns, so that 96-row
+// tiles number 160 or more: Qwen3-4B and 8B) from 17 rows: 96 weight rows
+// (48 outputs) per tile. Every tile reads the x rows of the call again from
+// L2, which with 32-row int8 tiles (32 B of weights per x row and k) was 4x
+// the weight bytes; 96 rows cut that to 1.3x. Same box, µs, 8B / 4B, against
+// the 32- and 64-row tiles: M = 24 33.7 -> 31.5 / 22.9 -> 22.2 (96 x 32, 3
+// stages); M = 40 47.5 -> 35.5 / 33.5 -> 25.4 (96 x 48, 3 stages); M = 64
+// 51.8 -> 40.4 / 36.7 -> 29.3 (96 x 64); M = 96 81.5 -> 48.5 / 58.6 -> 35.9
+// (96 x 96); M = 128 85.3 -> 78.6 / 60.0 -> 56.2 (96 x 64, two row tiles;
+// 96 x 96 there 90.9 / 67.4). At 16 rows 96 x 16 was slower (29.8 / 18.9
+// against 26.6 / 18.5).
 template <bool GATEUP, bool W8>
 int launch_splitk(const StreamArgs& a, hipStream_t s) {
   if constexpr (W8 && GATEUP) {
+    if (a.M > 16 && a.N >= 7680) {
+      if (a.M <= 32) return launch_splitk_cfg<96, 32, 4, 3, true, true>(a, s);
+      if (a.M <= 48) return launch_splitk_cfg<96, 48, 4, 3, true, true>(a, s);
+      if (a.M <= 64 || a.M > 96) return launch_splitk_cfg<96, 64, 4, 2, true, true>(a, s);
+      return launch_splitk_cfg<96, 96, 4, 2, true, true>(a, s);
+    }
     if (a.M <= 16) return launch_splitk_cfg<32, 16, 8, 2, true, true>(a, s);
     if (a.M <= 32) return launch_splitk_cfg<32, 32, 4, 3, true, true>(a, s);
     if (a.M <= 64) return launch_splitk_cfg<32, 64, 8, 2, true, true>(a, s);

@@ -579,6 +579,29 @@ def test_int8_split_k_tiles(M):
                f"int8 linear M={M} K={Kl} N={N}")
 
 
+@pytest.mark.parametrize("M", [17, 32, 40, 64, 65, 96, 100, 128])
+def test_int8_split_k_wide_gate_up_tiles(M):
+    """The int8 split-K tiles of 96 weight rows (48 outputs) that wide
+    gate-up outputs take from 17 rows: x tiles of 32, 48, 64 and 96 rows
+    (128 rows as two 64-row tiles), ragged outputs (9700 columns: a partial
+    last tile), an all-zero weight row, the cross-wave sum in passes (96 x 96
+    partials exceed one LDS stage). Checked against the oracle on a row
+    subset and for repeatability."""
+    kern = _kernels()
+    K, N = 2560, 9700
+    x, wg, wu = ffn_inputs(540 + M, M, K, N)
+    wu[17] = 0
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    xd = x.to(DEV)
+    y = kern.fused_gate_up_silu_w8(xd, qg, sg, qu, su)
+    assert torch.equal(y.view(torch.int16), kern.fused_gate_up_silu_w8(xd, qg, sg, qu, su).view(torch.int16))
+    rows = _rows(M, limit=40)
+    _check(y.cpu()[rows], ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                                       qu.cpu().numpy(), su.cpu().numpy()),
+           f"int8 wide split-K gate-up M={M} N={N}")
+
+
 @pytest.mark.parametrize("M", [129, 300, 1024])
 def test_int8_gemm_in_register(M):
     """The prefill gemm with int8 weight tiles dequantised in registers:
