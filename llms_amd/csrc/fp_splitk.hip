@@ -305,17 +305,22 @@ bool splitk_supported(const StreamArgs& a, bool aligned, bool w8) {
 // the 32- and 64-row tiles: M = 24 33.7 -> 31.5 / 22.9 -> 22.2 (96 x 32, 3
 // stages); M = 40 47.5 -> 35.5 / 33.5 -> 25.4 (96 x 48, 3 stages); M = 64
 // 51.8 -> 40.4 / 36.7 -> 29.3 (96 x 64); M = 96 81.5 -> 48.5 / 58.6 -> 35.9
-// (96 x 96); M = 128 85.3 -> 78.6 / 60.0 -> 56.2 (96 x 64, two row tiles;
-// 96 x 96 there 90.9 / 67.4). At 16 rows 96 x 16 was slower (29.8 / 18.9
-// against 26.6 / 18.5).
+// (96 x 96); M = 112 76.7 -> 51.8 / 55.4 -> 38.7 (96 x 112, the LDS full);
+// M = 128 78.4 -> 59.6 / 56.2 -> 44.9 (96 x 128 with 3 waves, whose two
+// stages fit where 4 waves' do not; two tiles of 64 rows: 78.6 / 56.2).
+// Each weight is dequantised once per row tile, so one tile over all the
+// rows beats two. At 16 rows 96 x 16 was slower (29.8 / 18.9 against 26.6
+// / 18.5).
 template <bool GATEUP, bool W8>
 int launch_splitk(const StreamArgs& a, hipStream_t s) {
   if constexpr (W8 && GATEUP) {
     if (a.M > 16 && a.N >= 7680) {
       if (a.M <= 32) return launch_splitk_cfg<96, 32, 4, 3, true, true>(a, s);
       if (a.M <= 48) return launch_splitk_cfg<96, 48, 4, 3, true, true>(a, s);
-      if (a.M <= 64 || a.M > 96) return launch_splitk_cfg<96, 64, 4, 2, true, true>(a, s);
-      return launch_splitk_cfg<96, 96, 4, 2, true, true>(a, s);
+      if (a.M <= 64) return launch_splitk_cfg<96, 64, 4, 2, true, true>(a, s);
+      if (a.M <= 96) return launch_splitk_cfg<96, 96, 4, 2, true, true>(a, s);
+      if (a.M <= 112) return launch_splitk_cfg<96, 112, 4, 2, true, true>(a, s);
+      return launch_splitk_cfg<96, 128, 3, 2, true, true>(a, s);
     }
     if (a.M <= 16) return launch_splitk_cfg<32, 16, 8, 2, true, true>(a, s);
     if (a.M <= 32) return launch_splitk_cfg<32, 32, 4, 3, true, true>(a, s);

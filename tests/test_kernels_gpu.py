@@ -579,14 +579,14 @@ def test_int8_split_k_tiles(M):
                f"int8 linear M={M} K={Kl} N={N}")
 
 
-@pytest.mark.parametrize("M", [17, 32, 40, 64, 65, 96, 100, 128])
+@pytest.mark.parametrize("M", [17, 32, 40, 64, 65, 96, 100, 112, 113, 128])
 def test_int8_split_k_wide_gate_up_tiles(M):
     """The int8 split-K tiles of 96 weight rows (48 outputs) that wide
-    gate-up outputs take from 17 rows: x tiles of 32, 48, 64 and 96 rows
-    (128 rows as two 64-row tiles), ragged outputs (9700 columns: a partial
-    last tile), an all-zero weight row, the cross-wave sum in passes (96 x 96
-    partials exceed one LDS stage). Checked against the oracle on a row
-    subset and for repeatability."""
+    gate-up outputs take from 17 rows: x tiles of 32, 48, 64, 96 and 112 rows
+    with 4 waves and 128 rows with 3, ragged outputs (9700 columns: a partial
+    last tile), an all-zero weight row, the cross-wave sum in passes (the
+    partials of the larger tiles exceed one LDS stage). Checked against the
+    oracle on a row subset and for repeatability."""
     kern = _kernels()
     K, N = 2560, 9700
     x, wg, wu = ffn_inputs(540 + M, M, K, N)
