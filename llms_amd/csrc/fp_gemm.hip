@@ -384,9 +384,10 @@ __global__ __launch_bounds__(WN * WM * kWave) void gemm_kernel(StreamArgs a, int
 // 16x16x32 MFMA's result latency). Gate-up 192 x 256, bit-identical: 4B M =
 // 512 66.3 -> 62.9 us, M = 500 x 9700 70.4 -> 65.2, 8B M = 512 99.9 -> 95.4;
 // with 16 k-steps (0.6B, M = 2048) 29.4 -> 30.1, so four waves need at least
-// 32. QKV 192 x 256 at M = 2048 was even (61.0 us) and the 256 x 256 forms
-// slower, so of the 192 x 256 tiles only gate-up runs with four waves; the
-// 192 x 128 tile (96 accumulators per lane) has four waves only.
+// 32. QKV 192 x 256 with four waves is 1-3% faster (4B M = 2048 61.1 -> 60.4
+// us) and the 256 x 256 forms slower (4B QKV M = 8192 207 -> 219-225 us), so
+// the 192 x 256 tiles run four waves where the step count allows; the 192 x
+// 128 tile (96 accumulators per lane) has four waves only.
 // With four waves the k-step may also be 128 wide (BK = 128: four 32-wide
 // substeps, each one's MFMAs carrying the next one's fragment reads, the
 // barrier before the last), for the one-round grids of 96 x 128 and 128 x
@@ -1309,6 +1310,13 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf
     if (gateup && nkt % 2 == 0 && nkt >= 32 && one_round(kT160x256)) return GemmPlan{kT160x256, 0};
     if (k128 && one_round(kT128x160)) return GemmPlan{kT128x160, 0};
     if (k128 && one_round(kT160x128)) return GemmPlan{kT160x128, 0};
+    // QKV: two nearly whole rounds of 192 x 256 tiles (four waves) over 256 x
+    // 256 rounds plus a 128 x 128 tail (same box, µs, bit-identical
+    // plans aside: 4B M = 4096 120.7 -> 117.3, 8B M = 4096 178.4 -> 175.6)
+    if (!gateup && nkt % 2 == 0 && nkt >= 32 && best.tile == kT256x256) {
+      const int64_t n = tile_count(kT192x256, M, N, false);
+      if (n > kCUs && n <= 2 * kCUs && n >= 2 * kCUs - kCUs / 16) return GemmPlan{kT192x256, 0};
+    }
   }
   return best;
 }
@@ -1389,10 +1397,12 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
           return launch_tiles_cfg<160, 256, 1, 4, true, false>(a, s);
       return (int)hipErrorInvalidValue;
     case kT192x256:
-      // bf16 gate-up with an even number of at least 32 k-steps: four waves
-      if constexpr (GATEUP && !W8)
+      // bf16 with an even number of at least 32 k-steps: four waves (QKV
+      // too, same box, bit-identical: 4B M = 2048 61.1 -> 60.4 us, M = 4096
+      // 120.7 -> 117.3; 8B M = 2048 91.2 -> 88.4, M = 4096 178.4 -> 175.6)
+      if constexpr (!W8)
         if ((a.K / kBK) % 2 == 0 && a.K / kBK >= 32)
-          return launch_tiles_cfg<192, 256, 2, 2, true, false>(a, s);
+          return launch_tiles_cfg<192, 256, 2, 2, GATEUP, false>(a, s);
       return launch_tiles_cfg<192, 256, 2, 4, GATEUP, W8>(a, s);
     default: break;
   }

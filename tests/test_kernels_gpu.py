@@ -290,11 +290,11 @@ def test_qwen3_4b_prefill_8192_rows():
 # (gate-up 384, QKV 768), 192 x 256 (gate-up 512, QKV 1536 and 2048),
 # 256 x 256 (gate-up 1536) and 320 x 256 tiles (gate-up 1024 and 2048, QKV
 # 3072), and whole 256 x 256 rounds followed by a 128 x 128 tail launch (QKV
-# 4096). Qwen3-0.6B: 64 x 64 (gate-up 96 and 320, QKV 128) and 128 x 128
+# 3800; at 4096 rows two rounds of 192 x 256 run instead). Qwen3-0.6B: 64 x 64 (gate-up 96 and 320, QKV 128) and 128 x 128
 # (gate-up 512, QKV 640) with 128-wide k-steps, 128 x 128 (gate-up 1024, QKV
 # 1536 and 3072) and 192 x 256 (gate-up 2048).
 PLAN_ROWS = {"gate_up": (QWEN3_4B, 2048, [128, 384, 512, 1024, 1536]),
-             "qkv": (QWEN3_4B, 4096, [160, 256, 384, 640, 768, 1536, 2048, 3072]),
+             "qkv": (QWEN3_4B, 3800, [160, 256, 384, 640, 768, 1536, 2048, 3072]),
              "gate_up_0.6b": (QWEN3_0_6B, 2048, [96, 320, 512, 1024]),
              "qkv_0.6b": (QWEN3_0_6B, 3072, [128, 640, 1536])}
 
@@ -912,6 +912,23 @@ def test_against_torch_gpu_path():
 
 # ----- persistent tile loops with few k-steps ---------------------------------
 
+
+
+@pytest.mark.parametrize("M,K,n_q,n_k", [
+    (2048, 2560, 4096, 1024),   # Qwen3-4B: one round of 192 x 256 tiles, four waves
+    (4096, 4096, 4096, 1024),   # Qwen3-8B: two rounds (not 256 x 256 + tail), 64 k-steps
+    (2000, 2560, 4000, 1000),   # partial tiles in M and N
+    (2048, 2496, 4096, 1024)])  # 39 k-steps (odd): eight waves
+def test_qkv_four_wave_tiles(M, K, n_q, n_k):
+    """bf16 QKV calls planned on 192 x 256 tiles run four waves per
+    workgroup (96 x 128 per wave, accumulators in AGPRs) with an even count
+    of at least 32 k-steps, else eight: against the oracle, and repeated
+    calls bit-identical."""
+    x, w = qkv_inputs(240 + M + K, M, K, n_q, n_k)
+    y = run_qkv(x, w, n_q, n_k)
+    assert torch.equal(y.view(torch.int16), run_qkv(x, w, n_q, n_k).view(torch.int16))
+    rows = _rows(M)
+    _check(y[rows], ref.ref_qkv_full(bits(x)[rows], bits(w), n_q, n_k), f"qkv 192 x 256 M={M} K={K}")
 
 @pytest.mark.parametrize("K", [64, 128, 192, 320])
 def test_tile_loops_few_ksteps(K):
