@@ -155,10 +155,17 @@ def test_qwen3_4b_qkv_decode(M):
     check_qkv(M, M, K, n_q, n_k)
 
 
-@pytest.mark.parametrize("M", [1, 3, 4, 5, 8])
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 8, 12, 16])
 def test_qwen3_4b_gate_up_decode(M):
     K, _, _, I = QWEN3_4B
     check_ffn(M, M, K, I)
+
+
+@pytest.mark.parametrize("M", [8, 16])
+def test_gate_up_verify_tiles_ragged(M):
+    """The 96-row split-K tiles of wide short-K gate-up at 8-16 rows with a
+    partial last tile (9700 outputs: 48 per tile), against the oracle."""
+    check_ffn(90 + M, M, 2560, 9700, label=f"gate-up verify tiles M={M} N=9700")
 
 
 def _bf16_from_bits(b: np.ndarray) -> torch.Tensor:
