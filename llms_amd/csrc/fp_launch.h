@@ -62,7 +62,8 @@ int launch_tiled(const StreamArgs& a, bool aligned, hipStream_t s);
 
 // Split-K MFMA tiles for the middle regime (fp_splitk.hip). bf16: used by
 // launch_stream from kSplitkMinM rows (kSplitkMinMSmallN for calls with at
-// most kSplitkSmallN weight rows) and by launch_tiled for small-N calls up to
+// most kSplitkSmallN weight rows; wider gate-up from 4 rows with K > 3072,
+// else 6) and by launch_tiled for small-N calls up to
 // kSplitkMaxM rows with K >= kSplitkMinKTiled, when splitk_supported() holds.
 constexpr int64_t kSplitkMinM = 8;
 constexpr int64_t kSplitkMinMSmallN = 3;

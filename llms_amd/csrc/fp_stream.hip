@@ -364,7 +364,13 @@ int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
     return launch_gemm<GATEUP, false>(a, s);
   // bf16 from 3 (small N, e.g. QKV) or 8 rows: split-K tiles (fp_splitk.hip)
   const int64_t wrows = GATEUP ? 2 * a.N : a.N;
-  const int64_t min_m = wrows <= kSplitkSmallN ? kSplitkMinMSmallN : kSplitkMinM;
+  // (wide gate-up from fewer rows: 4 with K > 3072, 6 below. One box, µs,
+  // stream -> split-K tiles: Qwen3-8B M = 4 34.0 -> 33.2, M = 6 35.1 -> 32.8,
+  // M = 7 36.3-37.4 -> 33.0, M = 3 33.0 -> 34.0; Qwen3-4B M = 7 21.0 -> 20.2,
+  // M = 6 even, M = 4 19.3 -> 20.1)
+  const int64_t min_m = wrows <= kSplitkSmallN ? kSplitkMinMSmallN
+                        : GATEUP               ? (a.K > 3072 ? 4 : 6)
+                                               : kSplitkMinM;
   if (!W8 && a.M >= min_m && splitk_supported(a, aligned, false))
     return launch_splitk<GATEUP, false>(a, s);
   // (int8 dequantisation needs registers of its own: 2 k-blocks per buffer)
