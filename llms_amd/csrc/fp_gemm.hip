@@ -1323,6 +1323,16 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf
 
 template <bool GATEUP, bool W8>
 int launch_gemm(const StreamArgs& a, hipStream_t s) {
+  if constexpr (W8 && GATEUP) {
+    // int8 gate-up up to 256 rows on one round of 192 x 128 dequantise-once
+    // tiles (8 waves of 96 x 32) where it gives 192-256 of them, instead of
+    // 128 x 128 gemm_kernel tiles that dequantise each fragment in every wave
+    // that reads it. Same box, µs, bit-identical: 8B M = 192 77.0 -> 62.8,
+    // M = 256 80.7 -> 67.2; 4B M = 192 49.7 -> 43.3, M = 256 50.4 -> 44.3
+    // (at 384 rows, more than a round, 8B 92 -> 117).
+    const int64_t n = tile_count(kT192x128, a.M, a.N, true);
+    if (a.M <= 256 && n >= 192 && n <= kCUs) return launch_tiles_cfg<192, 128, 2, 4, true, true>(a, s);
+  }
   const GemmPlan p = gemm_plan_unsplit(a.M, a.N, a.K, GATEUP, !W8);
   if constexpr (!W8) {
     switch (p.tile) {

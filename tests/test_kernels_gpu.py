@@ -609,6 +609,26 @@ def test_int8_split_k_wide_gate_up_tiles(M):
            f"int8 wide split-K gate-up M={M} N={N}")
 
 
+@pytest.mark.parametrize("M,K,N", [(129, 2560, 9728), (200, 2560, 9700), (256, 4096, 12288)])
+def test_int8_gate_up_192x128_tiles(M, K, N):
+    """int8 gate-up at 129-256 rows on one round of 192 x 128 dequantise-once
+    tiles (Qwen3-4B: 204 tiles, ragged outputs; Qwen3-8B: 256): bit-identical
+    to the bf16 call on the dequantised weights (the same k order), and a row
+    subset against the oracle."""
+    kern = _kernels()
+    x, wg, wu = ffn_inputs(560 + M, M, K, N)
+    xd = x.to(DEV)
+    qg, sg = kern.quantize_w8_per_row(wg.to(DEV))
+    qu, su = kern.quantize_w8_per_row(wu.to(DEV))
+    y = kern.fused_gate_up_silu_w8(xd, qg, sg, qu, su)
+    yb = kern.triton_fused_gate_up_silu(xd, kern.dequantize_w8(qg, sg), kern.dequantize_w8(qu, su))
+    assert torch.equal(y.view(torch.int16), yb.view(torch.int16)), f"int8 192 x 128 M={M} N={N}"
+    rows = _rows(M, limit=32)
+    _check(y.cpu()[rows], ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                                       qu.cpu().numpy(), su.cpu().numpy()),
+           f"int8 gate-up 192 x 128 M={M} K={K} N={N}")
+
+
 @pytest.mark.parametrize("M", [129, 300, 1024])
 def test_int8_gemm_in_register(M):
     """The prefill gemm with int8 weight tiles dequantised in registers:
