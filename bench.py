@@ -504,6 +504,7 @@ PROFILE_SET = [
     ("8B M=64", "qwen3-8b", 64, False, 1),
     ("8B M=256", "qwen3-8b", 256, False, 1),
     ("8B int8 M=64", "qwen3-8b", 64, True, 1),
+    ("8B int8 M=256", "qwen3-8b", 256, True, 1),
     ("prefill M=8192", "qwen3-4b", 8192, False, 1),
     ("8B TP=2 shard M=512", "qwen3-8b", 512, False, 2),
     ("8B TP=4 shard M=512", "qwen3-8b", 512, False, 4),
