@@ -28,7 +28,9 @@ import sys
 import time
 
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, GB/s
-PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+# MI355X dense bf16 MFMA, TFLOP/s: 256 CUs x 4 SIMDs x 1024 FLOP/clk x 2.4 GHz
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_CLOCK_GHZ = 2.4
 METRIC = "HBM GB/s (% peak) fused QKV+gate-up-SiLU Qwen3-4B M=1; TFLOPS at M=2048"
 
 # (K, n_q, n_k, I)
@@ -230,6 +232,44 @@ def cpu_baseline(torch, stacks: dict, reps: int) -> dict:
                    f"{first}; cpu: {cpu_model()}"),
         "configs": per,
     }
+
+
+def clock_under_load(torch, graph, replays: int = 8) -> dict:
+    """The shader clock while `graph` runs: the graph is replayed `replays`
+    times on the current stream while a second stream (default priority)
+    runs two one-thread spins back to back (torch.cuda._sleep: a fixed
+    number of shader cycles by clock64, i.e. s_memtime). HIP events on that
+    stream bracket the second spin, so the first absorbs any delay before the
+    side stream's work starts. GHz = cycles / elapsed time. The spin is one
+    wave on one CU; the replays leave room for it (one workgroup per CU).
+    The same measurement after the replays drain gives the clock of the spin
+    alone."""
+    side = torch.cuda.Stream()
+    cycles = 8_000_000
+
+    def spins():
+        e1 = torch.cuda.Event(enable_timing=True)
+        e2 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(side):
+            torch.cuda._sleep(cycles // 4)
+            e1.record()
+            torch.cuda._sleep(cycles)
+            e2.record()
+        return e1, e2
+
+    for _ in range(replays):
+        graph.replay()
+    e1, e2 = spins()
+    torch.cuda.synchronize()
+    loaded = cycles / (e1.elapsed_time(e2) / 1e3) / 1e9
+    e1, e2 = spins()
+    torch.cuda.synchronize()
+    idle = cycles / (e1.elapsed_time(e2) / 1e3) / 1e9
+    ok = 0.3 < loaded < 3.5
+    return {"ghz_under_load": round(loaded, 3) if ok else None,
+            "ghz_spin_alone": round(idle, 3) if 0.3 < idle < 3.5 else None,
+            "method": "torch.cuda._sleep (s_memtime cycles) on a side stream during the "
+                      "prefill graph replays, HIP events around the second of two spins"}
 
 
 def counters_run(torch, kern, shape, layers: int, Mp: int = 2048, blt: bool = False) -> dict:
@@ -442,56 +482,6 @@ def ship_gate_run(torch, kern, warmup: int = 50, iters: int = 200) -> dict:
     return out
 
 
-def read_ceiling_run(torch, kern, reps: int) -> dict:
-    """The read-only ceiling of the decode launches: libllms_amd_probe.so's
-    read kernel (the row-streaming kernels' memory pattern, no arithmetic)
-    over the same 36 cycled Qwen3-4B weight buffers, gate-up-shaped (Wg and Wu
-    rows read as pairs, 99.6 MB) and QKV-shaped (31.5 MB), timed like the
-    projections (graph replay, HIP events on the replay stream); the fused
-    kernels on the same buffers alongside. An empty kernel gives the launch
-    floor."""
-    import ctypes
-
-    from llms_amd import build as B
-
-    if not B.PROBE_SO.exists():
-        raise RuntimeError(f"{B.PROBE_SO} is not built (python -m llms_amd.build)")
-    probe = ctypes.CDLL(str(B.PROBE_SO))
-    probe.fp_probe_read_rows.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
-                                         ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    probe.fp_probe_read_rows.restype = ctypes.c_int
-    K, n_q, n_k, inter = SHAPES["qwen3-4b"]
-    n_qkv = n_q + 2 * n_k
-    L = 36
-    stack = Stack(torch, SHAPES["qwen3-4b"], L, M=1)
-    sink = torch.empty(inter, dtype=torch.int32, device="cuda")
-    row_kb = K * 2 // 1024
-
-    def rd(p0, p1, rows):
-        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-        rc = probe.fp_probe_read_rows(p0.data_ptr(), p1.data_ptr() if p1 is not None else None,
-                                      rows, row_kb, sink.data_ptr(), st)
-        assert rc == 0, rc
-
-    out = {"mode": "read_ceiling", "weight_sets": L, "shape": "qwen3-4b"}
-    t = kernel_seconds(torch, [lambda l=l: rd(stack.wg[l], stack.wu[l], inter) for l in range(L)], reps)
-    out["read_gate_up_us"] = round(t * 1e6, 3)
-    out["read_gate_up_gbs"] = round(2 * inter * K * 2 / t / 1e9, 1)
-    t = kernel_seconds(torch, [lambda l=l: rd(stack.wqkv[l], None, n_qkv) for l in range(L)], reps)
-    out["read_qkv_us"] = round(t * 1e6, 3)
-    out["read_qkv_gbs"] = round(n_qkv * K * 2 / t / 1e9, 1)
-    t = kernel_seconds(torch, [lambda l=l: kern.triton_fused_gate_up_silu(stack.x_ffn, stack.wg[l], stack.wu[l])
-                               for l in range(L)], reps)
-    out["fused_gate_up_us"] = round(t * 1e6, 3)
-    t = kernel_seconds(torch, [lambda l=l: kern.triton_fused_qkv(stack.x_attn, stack.wqkv[l], n_q=n_q, n_k=n_k)
-                               for l in range(L)], reps)
-    out["fused_qkv_us"] = round(t * 1e6, 3)
-    # launch floor: the probe on one row (one workgroup, 8 KB)
-    t = kernel_seconds(torch, [lambda l=l: rd(stack.wqkv[l], None, 1) for l in range(L)], reps)
-    out["one_row_launch_us"] = round(t * 1e6, 3)
-    return out
-
-
 # The kernel families profiled under profiles/ besides the default bench's
 # decode and prefill grids: (label, model, M, int8, tensor-parallel degree of
 # the per-GPU shard, 1 for the whole layer).
@@ -701,9 +691,6 @@ def main() -> int:
     ap.add_argument("--profile-set", action="store_true",
                     help="the fixed kernel sequence the profiles/ summaries other than the "
                          "default bench's are taken from (one JSON line per entry)")
-    ap.add_argument("--read-ceiling", action="store_true",
-                    help="time the read-only probe (the decode kernels' memory pattern, no "
-                         "arithmetic) on the decode weight buffers; prints one JSON line")
     ap.add_argument("--linear", metavar="M,N,K",
                     help="time only the plain projection (down / o) of this shape over "
                          "cycled weight sets and print one JSON line (profiling aid)")
@@ -744,9 +731,6 @@ def main() -> int:
         return 0
     if args.profile_set:
         profile_set_run(torch, kern, args.steps)
-        return 0
-    if args.read_ceiling:
-        print(json.dumps(read_ceiling_run(torch, kern, args.steps)), flush=True)
         return 0
     if args.ship_gate:
         print(json.dumps(ship_gate_run(torch, kern)), flush=True)
@@ -800,8 +784,10 @@ def main() -> int:
         psteps = max(3, args.steps // 4)
         psec = time_graph(torch, graph, psteps, warm_replays(torch, graph, max(1, args.warmup // 2)))
         tflops = L * pair_flops(Mp, K, n_qkv, inter) / psec / 1e12
+        clk = clock_under_load(torch, graph)
         dp_gu = kernel_seconds(torch, gu, 3)
         dp_qk = kernel_seconds(torch, qk, 3)
+        ghz = clk["ghz_under_load"]
         prefill = {
             "M": Mp,
             "tflops": round(tflops, 1),
@@ -811,6 +797,12 @@ def main() -> int:
             "gate_up_tflops": round(2 * Mp * K * 2 * inter / dp_gu / 1e12, 1),
             "qkv_us": round(dp_qk * 1e6, 2),
             "qkv_tflops": round(2 * Mp * K * n_qkv / dp_qk / 1e12, 1),
+            "peak_tflops": PEAK_BF16_TFLOPS,
+            "clock": clk,
+            # the same throughput against the matrix core's peak at the clock
+            # measured during the replays (None if the measurement failed)
+            "frac_of_peak_at_clock": (round(tflops / (PEAK_BF16_TFLOPS * ghz / PEAK_CLOCK_GHZ), 4)
+                                      if ghz else None),
         }
         log(f"prefill M={Mp}: {prefill}")
         del graph

@@ -61,7 +61,9 @@ typedef enum fp_status {
 /* Human-readable text for an fp_status value (static storage). */
 const char* fp_status_string(int status);
 
-/* ABI version of this library: (major << 16) | minor. */
+/* ABI version of this library: (major << 16) | minor. Minor 5 adds
+ * fp_rmsnorm_qkv_bf16_noalloc and FP_ERR_SCRATCH, and sizes
+ * fp_rmsnorm_workspace_bytes for the normalised rows of every call. */
 int fp_abi_version(void);
 
 /*
@@ -263,8 +265,10 @@ int fp_rmsnorm_gate_up_silu_w8(const void* x, int64_t ldx, const void* gamma, fl
  * capture, tight serving loops, harnesses that forbid allocation). Same
  * arguments, contract and results as fp_rmsnorm_qkv_bf16, bit for bit, but
  * the workspace is the library's own static device array of FP_SCRATCH_BYTES
- * (one per GPU, held until the process ends; its address is looked up once
- * per device on the first call there). Calls whose
+ * (one per GPU, held until the process ends; its address is looked up on
+ * the first successful call on a device, a failed lookup is retried by the
+ * next call). The stream, when not NULL, must belong to the current device
+ * (FP_ERR_DEVICE otherwise: the scratch address is per device). Calls whose
  * fp_rmsnorm_workspace_bytes(M, n_q + 2*n_k, K, 0, 0) exceeds FP_SCRATCH_BYTES
  * return FP_ERR_SCRATCH before anything is launched. Every call on a GPU
  * overwrites that GPU's scratch: calls that can overlap on one GPU (streams

@@ -1,15 +1,12 @@
 """Build the native parts of llms_amd in-tree.
 
-Three shared libraries are produced next to this file:
+Two shared libraries are produced next to this file:
 
 - ``libllms_amd_fp.so``: the HIP kernels for gfx950 and the C ABI declared in
   ``include/llms_amd_fp.h`` (no torch dependency; any FFI can bind it).
 - ``_torch_ops.so``: the thin ``torch.ops.llms_amd.*`` custom ops that call
   that C ABI on torch's current HIP stream (links ``libllms_amd_fp.so`` via
   ``$ORIGIN``).
-- ``libllms_amd_probe.so``: a read-only bandwidth probe with the decode
-  kernels' memory pattern, used by ``bench.py --read-ceiling`` (a measurement
-  aid, outside the C ABI).
 
 Run ``python -m llms_amd.build`` (or ``__graft_entry__.build()``). hipcc
 cross-compiles for gfx950 without a GPU present.
@@ -32,8 +29,6 @@ HIPCC = ROCM / "bin" / "hipcc"
 
 CAPI_SO = PKG / "libllms_amd_fp.so"
 TORCH_OPS_SO = PKG / "_torch_ops.so"
-# measurement aid for bench.py --read-ceiling (not part of the C ABI)
-PROBE_SO = PKG / "libllms_amd_probe.so"
 
 HIP_SOURCES = ["fp_api.hip", "fp_stream.hip", "fp_rows.hip", "fp_splitk.hip", "fp_tiled.hip",
                "fp_gemm.hip", "fp_scratch.hip"]
@@ -94,17 +89,6 @@ def build_capi(verbose: bool = False) -> Path:
     return CAPI_SO
 
 
-def build_probe(verbose: bool = False) -> Path:
-    """Compile the read-only bandwidth probe into ``libllms_amd_probe.so``."""
-    tmp = PROBE_SO.with_suffix(".so.tmp")
-    cmd = [str(HIPCC), *HIP_FLAGS, "-shared", str(CSRC / "fp_probe.hip"), "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd))
-    _run(cmd, "hipcc (libllms_amd_probe.so)")
-    os.replace(tmp, PROBE_SO)
-    return PROBE_SO
-
-
 def _torch_flags() -> tuple[list[str], list[str]]:
     import torch
     from torch.utils import cpp_extension
@@ -143,7 +127,7 @@ def build_torch_ops(verbose: bool = False) -> Path:
 
 def build_all(verbose: bool = False) -> list[Path]:
     """Build the libraries (always recompiles)."""
-    return [build_capi(verbose), build_torch_ops(verbose), build_probe(verbose)]
+    return [build_capi(verbose), build_torch_ops(verbose)]
 
 
 if __name__ == "__main__":

@@ -249,7 +249,7 @@ const char* fp_status_string(int status) {
   }
 }
 
-int fp_abi_version(void) { return (1 << 16) | 4; }
+int fp_abi_version(void) { return (1 << 16) | 5; }
 
 int64_t fp_workspace_bytes(int64_t M, int64_t N, int64_t K, int gate_up) {
   if (M < 1 || N < 1 || K < 1) return 0;

@@ -8,10 +8,11 @@
 // uses its name as an address (on the host it is only a registration
 // stand-in): the device address is looked up once per device with
 // hipGetSymbolAddress, with that device current, and that address is what
-// the kernels get. Every call on a GPU shares that GPU's array and overwrites
-// it (the normalised rows, then any split-k partials: both are written in
-// full before they are read, so nothing needs clearing between calls); calls
-// that can overlap on one GPU (different streams, no ordering) race on it.
+// the kernels get; a stream passed in must belong to the current device.
+// Every call on a GPU shares that GPU's array and overwrites it (the
+// normalised rows, then any split-k partials: both are written in full before
+// they are read, so nothing needs clearing between calls); calls that can
+// overlap on one GPU (different streams, no ordering) race on it.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -24,22 +25,33 @@ namespace {
 static __device__ __align__(256) unsigned char scratch[FP_SCRATCH_BYTES];
 
 constexpr int kMaxDevices = 64;
-std::once_flag g_once[kMaxDevices];
+std::mutex g_mu;
 void* g_ptr[kMaxDevices];
-hipError_t g_err[kMaxDevices];
 
-// The current device's address of `scratch` (looked up on the first call on
-// that device, with it current). FP_ERR_DEVICE if there is no current device
-// or the lookup fails.
-int device_scratch(void** out) {
+// The address of `scratch` on the device that runs the call: the current
+// device, which must also own `stream` when one is given (a stream of another
+// GPU would get this GPU's address: FP_ERR_DEVICE instead). Looked up on the
+// first successful call on that device, with it current; a failed lookup is
+// not remembered, so a later call tries again. FP_ERR_DEVICE if there is no
+// current device, the stream's device cannot be read or differs, or the
+// lookup fails.
+int device_scratch(void* stream, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FP_ERR_DEVICE;
-  std::call_once(g_once[dev], [dev] {
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess || sdev != dev)
+      return FP_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_ptr[dev] == nullptr) {
     void* p = nullptr;
-    g_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();  // leave no sticky error for the caller's next call
+      return FP_ERR_DEVICE;
+    }
     g_ptr[dev] = p;
-  });
-  if (g_err[dev] != hipSuccess || g_ptr[dev] == nullptr) return FP_ERR_DEVICE;
+  }
   *out = g_ptr[dev];
   return FP_OK;
 }
@@ -59,7 +71,7 @@ int fp_rmsnorm_qkv_bf16_noalloc(const void* x, int64_t ldx, const void* gamma, f
   const int64_t need = fp_rmsnorm_workspace_bytes(M, n_q + 2 * n_k, K, 0, 0);
   if (need > (int64_t)FP_SCRATCH_BYTES) return FP_ERR_SCRATCH;
   void* ptr = nullptr;
-  const int st = device_scratch(&ptr);
+  const int st = device_scratch(stream, &ptr);
   if (st != FP_OK) return st;
   return fp_rmsnorm_qkv_bf16(x, ldx, gamma, eps, w, ldw, y, ldy, M, n_q, n_k, K, ptr,
                              (int64_t)FP_SCRATCH_BYTES, stream);

@@ -46,6 +46,10 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), f"{name} declared in include/ but not exported"
         assert name in _lib.CAPI_SIGNATURES, f"{name} has no ctypes signature"
     assert lib.fp_abi_version() >> 16 == 1
+    # minor 5: the allocation-free entry point, FP_ERR_SCRATCH and the
+    # fused-norm workspace sizing that covers the normalised rows
+    if hasattr(lib, "fp_rmsnorm_qkv_bf16_noalloc"):
+        assert lib.fp_abi_version() & 0xFFFF >= 5
 
 
 def test_workspace_bytes_plan():

@@ -81,13 +81,18 @@ def test_noalloc_matches_workspace_entry(shape):
     equals the workspace entry point bit for bit and passes the oracle. The
     shapes cover the normalised-rows scratch (4B at 300 rows: the norm
     kernel, then the MFMA grid), the whole scratch (8B at 4096 rows: 32 MiB
-    of normalised rows), the k split across workgroups with its partials in
-    scratch (8B at 256 rows: 2 MiB of rows + 30 MiB of partials) and a small
-    last call (3 or 5 rows: the streaming kernel) over what the earlier calls
-    left in the scratch."""
-    K, n_q, n_k, Ms = {"4b": (2560, 4096, 1024, (300, 3)),
-                       "8b": (4096, 4096, 1024, (4096, 256, 5))}[shape]
+    of normalised rows), the k split across workgroups with its fp32 partials
+    in the scratch after the rows (4B and 8B at 128 rows: 0.6 or 1 MiB of
+    rows + 6 MiB of partials; asserted to split) and a small last call (3 or
+    5 rows: the streaming kernel) over what the earlier calls left in the
+    scratch."""
+    K, n_q, n_k, Ms = {"4b": (2560, 4096, 1024, (300, 128, 3)),
+                       "8b": (4096, 4096, 1024, (4096, 128, 5))}[shape]
     N = n_q + 2 * n_k
+    lib = _lib().capi()
+    # 128 rows split k across workgroups: the scratch holds partials beyond
+    # the normalised rows (so the case cannot silently stop splitting)
+    assert lib.fp_rmsnorm_workspace_bytes(128, N, K, 0, 0) > 128 * K * 2
     _, w = qkv_inputs(900 + K, 1, K, n_q, n_k)
     g = randn_bf16(gen(901 + K), K, std=0.5) + 1.0
     wd, gd = w.to(DEV), g.to(torch.bfloat16).to(DEV)
@@ -106,3 +111,46 @@ def test_noalloc_matches_workspace_entry(shape):
         p = ref.check_parity(bits(ya.cpu())[rows], out)
         print(f"noalloc {shape} M={M}: {p}")
         assert p.ok, p
+
+
+@pytest.mark.gpu
+def test_noalloc_in_graph_capture():
+    """The advertised use: the allocation-free call captured in a HIP graph
+    (torch.cuda.graph) and replayed. Every replay, with eager work and
+    synchronisations between replays, equals the eager workspace entry point
+    bit for bit; replays of the same graph after the scratch was overwritten
+    by an eager call of another size still give the captured call's result.
+    4B QKV at 128 rows: the norm kernel, then k split across workgroups with
+    its partials in the scratch."""
+    K, n_q, n_k, M = 2560, 4096, 1024, 128
+    N = n_q + 2 * n_k
+    x, w = qkv_inputs(950, M, K, n_q, n_k)
+    g = randn_bf16(gen(951), K, std=0.5) + 1.0
+    xd, wd, gd = x.to(DEV), w.to(DEV), g.to(torch.bfloat16).to(DEV)
+    ref_y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    _call(True, xd, gd, wd, n_q, n_k, ref_y,
+          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    y = torch.zeros(M, N, dtype=torch.bfloat16, device=DEV)
+    # the first call on this device (symbol lookup) happens before capture
+    _call(False, xd, gd, wd, n_q, n_k, y, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        _call(False, xd, gd, wd, n_q, n_k, y, ctypes.c_void_p(s.cuda_stream))
+    torch.cuda.synchronize()
+    x2, _ = qkv_inputs(952, 300, K, n_q, n_k)
+    x2d = x2.to(DEV)
+    y2 = torch.empty(300, N, dtype=torch.bfloat16, device=DEV)
+    for r in range(4):
+        y.fill_(3.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref_y.view(torch.int16)), f"replay {r}"
+        # eager work on the same scratch between replays (another size)
+        _call(False, x2d, gd, wd, n_q, n_k, y2,
+              ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+    del graph
