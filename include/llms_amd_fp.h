@@ -172,18 +172,15 @@ int fp_linear_bf16_ws(const void* x, int64_t ldx,
                       void* stream);
 
 /*
- * Workspace variants of the int8 entry points (no reference counterpart). For
- * calls with enough rows (fp_workspace_bytes_w8(M, N, K, gate_up) > 0: from
- * 48 rows for one weight stream; 48-64 and from 256 or 512 rows for gate-up),
- * given that much
- * workspace, the int8 weights are dequantised once into the workspace as
- * bf16(q * s) — the exact weight the int8 contract computes with — and the
- * bf16 MFMA path runs on them; where that path would split k across at least
- * 4 workgroups, the split runs on the int8 weights directly (dequantised in
- * registers, bit-identical result) and the workspace holds only its fp32
- * partials. Results stay within the same contract. Without a workspace, or
- * with fewer rows, the in-register dequantising kernels of the plain entry
- * points run.
+ * Workspace variants of the int8 entry points (no reference counterpart).
+ * Every int8 call dequantises in registers (in the prefill tiles: once per
+ * workgroup into LDS); no bf16 copy of the weights is written anywhere. The
+ * workspace serves only the k split across workgroups: for the shapes whose
+ * plan splits k over at least 4 workgroups (fp_workspace_bytes_w8(M, N, K,
+ * gate_up) > 0: down and o projections at 96-768 rows, Qwen3-8B QKV at
+ * 129-256), given that much workspace, the split runs with its fp32
+ * partials there. Without it those calls run unsplit, with the same
+ * contract.
  */
 int64_t fp_workspace_bytes_w8(int64_t M, int64_t N, int64_t K, int gate_up);
 
@@ -221,8 +218,7 @@ int fp_linear_w8_ws(const void* x, int64_t ldx,
  * LDS) whose x, weights and gamma are 16-byte aligned with row strides that
  * are multiples of 8 (int8 weights: 16) run as one launch that normalises x
  * while staging it and need no workspace. Every other call needs a workspace
- * (the normalised rows, then any split-k partials, or for int8 calls with
- * enough rows the dequantised weights as in fp_qkv_w8_ws) and returns
+ * (the normalised rows, then any split-k partials) and returns
  * FP_ERR_WORKSPACE without one; fp_rmsnorm_workspace_bytes(M, N, K, gate_up,
  * int8) is enough for any pointers and strides of that shape. eps must be
  * finite and >= 0.

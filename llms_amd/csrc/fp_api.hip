@@ -34,43 +34,6 @@ __global__ __launch_bounds__(256) void quantize_w8_kernel(const uint16_t* w, int
   }
 }
 
-// bf16(q * s[row]) (K % 16 == 0, 16-byte-aligned rows): the weight the int8
-// kernels compute with, written as a bf16 matrix [N, K] (row stride K) for
-// the bf16 MFMA path. blockIdx.y picks the matrix (gate-up: Wg, Wu in one
-// launch); each thread converts two 16-weight chunks, half the matrix apart,
-// reading the int8 bytes (used once) with the non-temporal hint. Measured on
-// MI355X, 4B gate-up (2 x 9728 x 2560): two launches of one chunk per thread
-// 2 x 15.6 us.
-__global__ __launch_bounds__(256) void dequant_w8_kernel(const int8_t* q0, int64_t ldq0,
-                                                         const float* s0, uint16_t* w0,
-                                                         const int8_t* q1, int64_t ldq1,
-                                                         const float* s1, uint16_t* w1,
-                                                         int64_t N, int64_t K) {
-  const bool second = blockIdx.y != 0;
-  const int8_t* q = second ? q1 : q0;
-  const int64_t ldq = second ? ldq1 : ldq0;
-  const float* scale = second ? s1 : s0;
-  uint16_t* w = second ? w1 : w0;
-  const int64_t per_row = K / 16, total = N * per_row, half = (total + 1) / 2;
-  const int64_t t0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t0 >= half) return;
-  const int64_t t1 = t0 + half;
-  const bool two = t1 < total;
-  const int64_t r0 = t0 / per_row, c0 = (t0 - r0 * per_row) * 16;
-  const int64_t r1 = two ? t1 / per_row : r0, c1 = two ? (t1 - r1 * per_row) * 16 : c0;
-  const u32x4 v0 = ld16_nt(q + r0 * ldq + c0);
-  const u32x4 v1 = ld16_nt(q + r1 * ldq + c1);
-  const float sc0 = scale[r0], sc1 = scale[r1];
-  uint16_t* out0 = w + r0 * K + c0;
-  *reinterpret_cast<u32x4*>(out0) = dequant8_bf16(v0.x, v0.y, sc0, -128.f * sc0);
-  *reinterpret_cast<u32x4*>(out0 + 8) = dequant8_bf16(v0.z, v0.w, sc0, -128.f * sc0);
-  if (two) {
-    uint16_t* out1 = w + r1 * K + c1;
-    *reinterpret_cast<u32x4*>(out1) = dequant8_bf16(v1.x, v1.y, sc1, -128.f * sc1);
-    *reinterpret_cast<u32x4*>(out1 + 8) = dequant8_bf16(v1.z, v1.w, sc1, -128.f * sc1);
-  }
-}
-
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // rc is the hipError_t of the launch (hipGetLastError right after it).
@@ -91,38 +54,21 @@ int run(const StreamArgs& a, bool aligned, hipStream_t s) {
 
 inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
-// int8 calls with enough rows and a workspace: the weights are dequantised
-// once into the workspace and the bf16 path runs on them. The extra 3 bytes
-// per weight pay for themselves once the in-register int8 kernels are
-// compute-bound. Measured on MI355X (Qwen3-4B/8B): one weight stream (QKV,
-// down, o) from 48 rows (4B QKV at 48 rows: 23 vs 37 us; 4B down at 128:
-// 42 vs 226 us; QKV at 2048: 77 vs 133 us). Gate-up at 48-64 rows (the int8
-// streaming kernel's weakest range: 4B 74 vs 94 us at 64), then again from
-// 256 rows, or 512 above 2^26 weights; in between the int8 LDS tiles hold up
-// (8B gate-up at 256: 151 vs 143 us; at 2048: 397 vs 776 us).
-inline int64_t dequant_bytes(int64_t N, int64_t K, bool gateup) {
-  return round_up(N * K * 2, 256) * (gateup ? 2 : 1);
-}
-
-inline bool use_dequant(int64_t M, int64_t N, int64_t K, bool gateup) {
-  if (K % 16 != 0 || M < 48) return false;
-  // the int8 split-K tiles and the int8 gemm take these
-  if (splitk8_shape(M, N, K, gateup) || gemm8_shape(M, N, K, gateup)) return false;
-  if (!gateup || M <= kStreamMaxM) return true;
-  return M >= (2 * N * K > ((int64_t)1 << 26) ? 512 : 256);
-}
-
-// Of those, the calls whose bf16 plan splits k across at least 4 workgroups
-// run that split on the int8 weights directly (gemm_kernel dequantising in
-// registers; partials and result bit-identical to the split over the
-// dequantised weights) and need only the partials' workspace. Measured on
-// MI355X against dequantise-then-split: 8B QKV at 256 rows 44.1 -> 30.9 us,
-// 4B down at 128 40.5 -> 26.9 us, 8B down at 256 66.2 -> 46.9 us, 8B o at 256
-// 34.0 -> 26.7 us; with 2-3 splits (down at 1024 rows and more) the two are
-// even or the dequantised path 1-4% ahead, so it stays.
+// int8 calls always dequantise in registers (or once per workgroup into
+// LDS in the prefill tiles); no bf16 copy of the weights is ever written.
+// With a workspace, the calls whose plan splits k across at least 4
+// workgroups (gemm_split_plan: down and o at 96-512 rows, 8B QKV at 129-256)
+// run that split on the int8 weights (gemm_kernel dequantising in registers,
+// fp32 partials in the workspace, the fixed-order reduce). Excluded: the
+// shapes the int8 split-K tiles take (splitk8_shape) and those the
+// in-register prefill tiles take unsplit (gemm8_shape). Measured on MI355X
+// against the unsplit dispatch: 8B QKV at 256 rows 44.1 -> 30.9 us, 4B down
+// at 128 40.5 -> 26.9 us, 8B down at 256 66.2 -> 46.9 us, 8B o at 256 34.0 ->
+// 26.7 us.
 inline GemmSplit split8_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
   const GemmSplit none{-1, 1};
-  if (K % 64 != 0 || !use_dequant(M, N, K, gateup)) return none;
+  if (K % 64 != 0 || M < 48) return none;
+  if (splitk8_shape(M, N, K, gateup) || gemm8_shape(M, N, K, gateup)) return none;
   const GemmSplit p = gemm_split_plan(M, N, K, gateup);
   return p.nsplit >= 4 ? p : none;
 }
@@ -130,34 +76,14 @@ inline GemmSplit split8_plan(int64_t M, int64_t N, int64_t K, bool gateup) {
 template <bool GATEUP>
 int run_w8(const StreamArgs& a, bool aligned, void* ws, int64_t ws_bytes, hipStream_t s) {
   if (a.M == 0) return FP_OK;
-  const int64_t wb = dequant_bytes(a.N, a.K, GATEUP);
   const GemmSplit p8 = split8_plan(a.M, a.N, a.K, GATEUP);
-  if (aligned && p8.tile >= 0) {
+  if (aligned && p8.tile >= 0 && ws) {
     StreamArgs b = a;
     b.ws = (float*)ws;
-    b.ws_floats = ws ? ws_bytes / 4 : 0;
-    if (ws && gemm_split_ws_floats(p8, a.M, a.N, a.K, GATEUP) <= b.ws_floats &&
+    b.ws_floats = ws_bytes / 4;
+    if (gemm_split_ws_floats(p8, a.M, a.N, a.K, GATEUP) <= b.ws_floats &&
         gemm_supported(b, true, true))
       return launch_status(launch_gemm_split<GATEUP, true>(b, p8, s));
-  } else if (aligned && use_dequant(a.M, a.N, a.K, GATEUP) && ws && ws_bytes >= wb) {
-    uint16_t* w0 = (uint16_t*)ws;
-    uint16_t* w1 = GATEUP ? (uint16_t*)((char*)ws + wb / 2) : nullptr;
-    const unsigned blocks = (unsigned)(((a.N * (a.K / 16) + 1) / 2 + 255) / 256);
-    hipLaunchKernelGGL(dequant_w8_kernel, dim3(blocks, GATEUP ? 2 : 1), dim3(256), 0, s,
-                       (const int8_t*)a.w0, a.ldw0, a.s0, w0,
-                       (const int8_t*)(GATEUP ? a.w1 : a.w0), GATEUP ? a.ldw1 : a.ldw0,
-                       GATEUP ? a.s1 : a.s0, GATEUP ? w1 : w0, a.N, a.K);
-    int rc = (int)hipGetLastError();
-    if (rc) return launch_status(rc);
-    StreamArgs b = a;
-    b.w0 = w0;
-    b.ldw0 = a.K;
-    b.w1 = w1;
-    b.ldw1 = GATEUP ? a.K : 0;
-    b.s0 = b.s1 = nullptr;
-    b.ws = (float*)((char*)ws + wb);
-    b.ws_floats = (ws_bytes - wb) / 4;
-    return run<GATEUP, false>(b, true, s);
   }
   StreamArgs b = a;
   b.ws = nullptr;
@@ -166,11 +92,9 @@ int run_w8(const StreamArgs& a, bool aligned, void* ws, int64_t ws_bytes, hipStr
 }
 
 int64_t w8_workspace_bytes(int64_t M, int64_t N, int64_t K, bool gateup) {
-  if (M < 1 || N < 1 || K < 1 || !use_dequant(M, N, K, gateup)) return 0;
+  if (M < 1 || N < 1 || K < 1) return 0;
   const GemmSplit p8 = split8_plan(M, N, K, gateup);
-  if (p8.tile >= 0) return 4 * gemm_split_ws_floats(p8, M, N, K, gateup);
-  return dequant_bytes(N, K, gateup) +
-         4 * gemm_split_ws_floats(gemm_split_plan_bf16(M, N, K, gateup), M, N, K, gateup);
+  return p8.tile >= 0 ? 4 * gemm_split_ws_floats(p8, M, N, K, gateup) : 0;
 }
 
 // RMSNorm prologue + projection: one launch on the rows kernel (x normalised

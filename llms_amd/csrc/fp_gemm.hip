@@ -1310,13 +1310,17 @@ GemmPlan gemm_plan_unsplit(int64_t M, int64_t N, int64_t K, bool gateup, bool bf
     if (gateup && nkt % 2 == 0 && nkt >= 32 && one_round(kT160x256)) return GemmPlan{kT160x256, 0};
     if (k128 && one_round(kT128x160)) return GemmPlan{kT128x160, 0};
     if (k128 && one_round(kT160x128)) return GemmPlan{kT160x128, 0};
-    // QKV: two nearly whole rounds of 192 x 256 tiles (four waves) over 256 x
-    // 256 rounds plus a 128 x 128 tail (same box, µs, bit-identical
-    // plans aside: 4B M = 4096 120.7 -> 117.3, 8B M = 4096 178.4 -> 175.6)
-    if (!gateup && nkt % 2 == 0 && nkt >= 32 && best.tile == kT256x256) {
-      const int64_t n = tile_count(kT192x256, M, N, false);
-      if (n > kCUs && n <= 2 * kCUs && n >= 2 * kCUs - kCUs / 16) return GemmPlan{kT192x256, 0};
-    }
+  }
+  // QKV: two nearly whole rounds of 192 x 256 tiles (four waves) over 256 x
+  // 256 rounds plus a 128 x 128 tail (same box, µs, bit-identical
+  // plans aside: 4B M = 4096 120.7 -> 117.3, 8B M = 4096 178.4 -> 175.6).
+  // int8 too, on eight-wave dequantise-once tiles, in place of a 256 x 256
+  // round and a 128 x 128 tail of gemm_kernel, which dequantises every
+  // fragment in each wave that reads it (same box, bit-identical: 8B M =
+  // 4096 202.2 -> 181.6 us, 4B M = 4096 133.1 -> 120.6)
+  if (!gateup && nkt % 2 == 0 && nkt >= 32 && best.tile == kT256x256) {
+    const int64_t n = tile_count(kT192x256, M, N, false);
+    if (n > kCUs && n <= 2 * kCUs && n >= 2 * kCUs - kCUs / 16) return GemmPlan{kT192x256, 0};
   }
   return best;
 }
@@ -1410,6 +1414,8 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
       // bf16 with an even number of at least 32 k-steps: four waves (QKV
       // too, same box, bit-identical: 4B M = 2048 61.1 -> 60.4 us, M = 4096
       // 120.7 -> 117.3; 8B M = 2048 91.2 -> 88.4, M = 4096 178.4 -> 175.6)
+      // (int8 keeps eight waves: four measured slower, 8B QKV M = 4096
+      // 181.6 -> 198.5 us, 4B M = 2048 61.3 -> 69.0)
       if constexpr (!W8)
         if ((a.K / kBK) % 2 == 0 && a.K / kBK >= 32)
           return launch_tiles_cfg<192, 256, 2, 2, GATEUP, false>(a, s);
@@ -1437,10 +1443,15 @@ int launch_gemm(const StreamArgs& a, hipStream_t s) {
     if (GATEUP) t.w1 = static_cast<const uint16_t*>(a.w1) + p.nmain * a.ldw1;
   }
   t.y = a.y + p.nmain;
-  // int8 gate-up tails: 256 x 128 tiles of the dequantise-once tile kernel
-  // (the 128 x 128 gemm_kernel dequantises each weight fragment in every
-  // wave that reads it)
-  if constexpr (W8 && GATEUP) return launch_tiles_cfg<256, 128, 4, 2, true, true>(t, s);
+  // int8 gate-up tails on the dequantise-once tile kernel (the 128 x 128
+  // gemm_kernel dequantises each weight fragment in every wave that reads
+  // it): one round of 192 x 128 tiles where 192-256 of them cover it, else
+  // 256 x 128 tiles
+  if constexpr (W8 && GATEUP) {
+    const int64_t n = tile_count(kT192x128, t.M, t.N, true);
+    if (n >= 192 && n <= kCUs) return launch_tiles_cfg<192, 128, 2, 4, true, true>(t, s);
+    return launch_tiles_cfg<256, 128, 4, 2, true, true>(t, s);
+  }
   return launch_gemm_cfg<128, 128, 4, 2, GATEUP, 2, W8>(t, s);
 }
 

@@ -85,19 +85,14 @@ inline bool splitk8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (M < min_m || M > kSplitkMaxM8 || K % 64 != 0) return false;
   return M <= 64 || K <= 8192;
 }
-// Whether an int8 call of this shape runs the MFMA tiles with in-register
-// dequantisation in preference to dequantising the weights into a workspace
-// first. Measured on MI355X (Qwen3-4B/8B): gate-up from 129 to 1024 rows (8B
-// at 256 rows: 121.7 -> 75.9 us); one weight stream of more than 4096 rows
-// with K <= 2560 from 129 to 512 rows (4B QKV at 256: 33.7 -> 28.4 us), and
-// where its tiles are one round of 192 x 256 tiles on at least 3/4 of the
-// CUs (the one-tile-per-CU kernel, which dequantises each weight once per
-// workgroup: 4B QKV at 2048 rows 65.2 -> 60.8 us, bf16 60.3). Elsewhere with
-// more rows the dequantisation costs 4-16% against the bf16 path on
-// dequantised weights (4B QKV at 1024 rows 48.5 vs 50.6 us, 8B QKV at 4096
-// 176 vs 204, 4B gate-up at 2048 187 vs 203); the long-K down projections
-// keep that path with k split across workgroups. Without a workspace every
-// aligned int8 call of more than 128 rows runs the in-register tiles.
+// int8 shapes that run the unsplit MFMA tiles even where a workspace would
+// allow k split across workgroups (the split of fp_api.hip's split8_plan is
+// not taken for them): gate-up from 129 to 1024 rows, and one weight stream
+// of more than 4096 rows with K <= 2560 from 129 to 512 rows or where its
+// tiles are one round of 192 x 256 on at least 3/4 of the CUs (Qwen3-4B QKV).
+// Measured on MI355X when the alternative was dequantising into a bf16
+// workspace: 8B gate-up at 256 rows 121.7 -> 75.9 us, 4B QKV at 256 33.7 ->
+// 28.4 us, 4B QKV at 2048 65.2 -> 60.8 us.
 inline bool gemm8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (M <= kSplitkMaxM8 || K % 64 != 0) return false;
   if (gateup) return M <= 1024;

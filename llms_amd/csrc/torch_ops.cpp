@@ -65,8 +65,8 @@ at::Tensor workspace(const at::Tensor& x, int64_t M, int64_t N, int64_t K, bool 
   return at::empty({bytes}, x.options().dtype(at::kByte));
 }
 
-// Workspace for an int8 call: the dequantised weights (and split partials)
-// from 128 rows, empty below.
+// Workspace for an int8 call: the fp32 partials where k is split across
+// workgroups, empty otherwise (int8 weights are never expanded to bf16).
 at::Tensor workspace_w8(const at::Tensor& x, int64_t M, int64_t N, int64_t K, bool gate_up) {
   const int64_t bytes = fp_workspace_bytes_w8(M, N, K, gate_up ? 1 : 0);
   return at::empty({bytes}, x.options().dtype(at::kByte));

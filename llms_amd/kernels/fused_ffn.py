@@ -68,19 +68,10 @@ def fused_gate_up_silu_w8(
     su: torch.Tensor,
 ) -> torch.Tensor:
     """int8 weight-only gate-up-SiLU: the bf16 contract on the dequantised
-    weights ``bf16(q * s)``. Where they are dequantised depends on the row
-    count:
-
-    - In registers up to 1024 rows, so no bf16 copy exists.
-    - Above 1024 rows, into a bf16 workspace of 2 bytes per weight (99.6 MB
-      for Qwen3-4B), after which the bf16 kernels run. The torch op takes it
-      from the caching allocator. This is faster there: Qwen3-4B at 2048 rows
-      187 against 203 us, because the in-register tiles cannot use the
-      320 x 256 tile.
-
-    Every form computes the bf16 contract on bf16(q * s), the
-    dequantise-then-matmul result up to the fp32 summation order of the plan
-    that runs."""
+    weights ``bf16(q * s)``, dequantised in registers at every row count (in
+    the prefill tiles once per workgroup, into on-chip LDS): no bf16 copy of
+    the weights exists. The result is the dequantise-then-matmul result up
+    to the fp32 summation order of the plan that runs."""
     if qg.shape != qu.shape:
         raise ValueError(f"qg shape {tuple(qg.shape)} != qu shape {tuple(qu.shape)}")
     if qg.dim() != 2:

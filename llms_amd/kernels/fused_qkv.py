@@ -86,20 +86,10 @@ def fused_qkv_w8(
 
     ``q_qkv`` is the ``(n_q + 2*n_k, K)`` int8 weight and ``s_qkv`` its
     per-row fp32 scale (see :func:`llms_amd.kernels.quant.quantize_w8_per_row`).
-    Where the weights are dequantised depends on the row count:
-
-    - In registers up to 128 rows, and up to 512 rows for outputs wider than
-      4096 with K <= 2560 (Qwen3-4B QKV). No bf16 copy exists.
-    - Once per workgroup into on-chip LDS in the prefill tiles for those
-      outputs where the tiles fill one round of the chip (Qwen3-4B QKV at
-      1536-2048 rows). No bf16 copy exists there either.
-    - Otherwise, above 128 rows, into a bf16 workspace of 2 bytes per weight
-      (31.5 MB for Qwen3-4B QKV), which then runs the bf16 kernels. The torch
-      op takes it from the caching allocator. This is faster on those shapes;
-      Qwen3-4B QKV at 1024 rows: 48.5 against 50.6 us in registers.
-
-    Every form computes matmul on ``bf16(q * s)``, up to the fp32 summation
-    order of the plan that runs.
+    The weights are dequantised in registers at every row count (in the
+    prefill tiles once per workgroup, into on-chip LDS): no bf16 copy of the
+    weights exists. Every plan computes matmul on ``bf16(q * s)``, up to the
+    fp32 summation order of the plan that runs.
     """
     if q_qkv.dim() != 2:
         raise ValueError(

@@ -6,10 +6,9 @@ stay ``nn.Linear`` (hipBLASLt) in the reference's fused engine.
 Path: wrapper -> ``torch.ops.llms_amd.linear`` -> C ABI ``fp_linear_bf16`` ->
 the same row-streaming / split-K / LDS-tiled kernels as the QKV projection,
 with every output column a plain dot product (no epilogue). The int8 variant
-dequantises per-row int8 weights as the fused int8 projections do. That is in
-registers at decode and in the middle regime. At larger row counts it goes into
-a bf16 workspace first, or k is split across workgroups on the int8 weights.
-Either way the result equals matmul on ``bf16(q * s)``.
+dequantises per-row int8 weights in registers as the fused int8 projections
+do (no bf16 copy of the weights), with k split across workgroups where the
+plan says so. The result equals matmul on ``bf16(q * s)``.
 """
 
 from __future__ import annotations
@@ -47,9 +46,8 @@ def fused_linear(x: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
 
 
 def fused_linear_w8(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
-    """int8 weight-only ``x @ bf16(q * s[:, None]).T``. The weights are
-    dequantised in registers or, at larger row counts, into a bf16 workspace
-    first (see the module docstring)."""
+    """int8 weight-only ``x @ bf16(q * s[:, None]).T``, the weights
+    dequantised in registers (see the module docstring)."""
     if q.dim() != 2:
         raise ValueError(f"q must be 2D (N, K), got shape {tuple(q.shape)}")
     if x.shape[-1] != q.shape[1]:

@@ -52,6 +52,26 @@ def test_library_exports_every_declared_symbol():
         assert lib.fp_abi_version() & 0xFFFF >= 5
 
 
+def test_int8_workspace_is_split_partials_only():
+    """int8 calls never expand their weights to bf16: at every BASELINE int8
+    configuration (Qwen3-4B M = 1, 4, 2048; Qwen3-8B M = 1 ... 4096) and at
+    other row counts, fp_workspace_bytes_w8 is 0, or exactly the fp32
+    partials of k split over 4-16 workgroups (S planes of M x W floats, W =
+    N, gate-up 2N) where the split plan takes the call. No GPU needed."""
+    from llms_amd import _lib
+
+    lib = _lib.capi()
+    shapes = {"4b": (2560, 6144, 9728), "8b": (4096, 6144, 12288)}
+    for model, (K, n_qkv, inter) in shapes.items():
+        for M in (1, 3, 4, 8, 16, 64, 128, 129, 256, 512, 1024, 2048, 4096, 8192):
+            for N, gu in ((n_qkv, 0), (inter, 1)):
+                ws = lib.fp_workspace_bytes_w8(M, N, K, gu)
+                plane = 4 * M * N * (2 if gu else 1)
+                assert ws == 0 or (ws % plane == 0 and 4 <= ws // plane <= 16), (model, M, N, ws)
+                if gu or M in (1, 4, 2048, 4096) or model == "4b":
+                    assert ws == 0, (model, M, N, gu, ws)
+
+
 def test_workspace_bytes_plan():
     """The split-k plan (a host function: no GPU needed). Splits only where
     the unsplit grid leaves the chip idle and k is long: Qwen3 down from 32

@@ -559,7 +559,7 @@ def test_int8_split_k_tiles(M):
     dequantises its MFMA fragment): gate-up, QKV and the plain projection with
     output counts that leave partial tiles, an all-zero weight row, and for the
     projection both a short K (split-K from 5 rows) and a long K (split-K up to
-    64 rows, the dequantise-first path above)."""
+    64 rows, then the split across workgroups or the prefill tiles)."""
     kern = _kernels()
     K = 2048
     x, wg, wu = ffn_inputs(500 + M, M, K, 1000)
@@ -796,50 +796,108 @@ def test_split_k_across_workgroups(M, N, K, op):
     _check(y.cpu()[rows], ref.ref_linear(bits(x)[rows], bits(w)), f"split {op} M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("M,K,N,op,dq", [(47, 2576, 6144, "qkv", False), (48, 2576, 6144, "qkv", True),
-                                         (48, 2560, 6144, "qkv", False),
-                                         (64, 1040, 1001, "gate-up", True),
-                                         (200, 1040, 1001, "gate-up", False),
-                                         (256, 1040, 1001, "gate-up", True),
-                                         (128, 9728, 2560, "linear", True),
-                                         (128, 4096, 2560, "linear", False),
-                                         (512, 9728, 2560, "linear", True),
-                                         (300, 2560, 9728, "gate-up", False),
-                                         (1100, 2560, 1000, "gate-up", True),
-                                         (200, 2560, 4352, "qkv", False),
-                                         (600, 2560, 4352, "qkv", True)])
-def test_int8_dequantised_mfma_path(M, K, N, op, dq):
-    """With enough rows the int8 calls dequantise the weights into the
-    workspace and run the bf16 path (or, where that path splits k across at
-    least 4 workgroups, run the split on the int8 weights: see
-    test_int8_split_across_workgroups); the contract is unchanged. Below the threshold, where the int8 split-K
-    tiles take the shape (K % 64 == 0, up to 128 rows, K <= 8192 above 64) and
-    where the int8 gemm does (gate-up up to 1024 rows, one weight stream of
-    more than 4096 rows with K <= 2560 up to 512 rows), the in-register int8
-    kernels run."""
+@pytest.mark.parametrize("M,K,N,op,split", [(47, 2576, 6144, "qkv", False),
+                                            (48, 2576, 6144, "qkv", False),
+                                            (48, 2560, 6144, "qkv", False),
+                                            (64, 1040, 1001, "gate-up", False),
+                                            (200, 1040, 1001, "gate-up", False),
+                                            (256, 1040, 1001, "gate-up", False),
+                                            (128, 9728, 2560, "linear", True),
+                                            (128, 4096, 2560, "linear", False),
+                                            (512, 9728, 2560, "linear", True),
+                                            (1024, 9728, 2560, "linear", False),
+                                            (300, 2560, 9728, "gate-up", False),
+                                            (1100, 2560, 1000, "gate-up", False),
+                                            (200, 2560, 4352, "qkv", False),
+                                            (600, 2560, 4352, "qkv", False)])
+def test_int8_routes_in_register(M, K, N, op, split):
+    """Every int8 route dequantises in registers (once per workgroup into
+    LDS in the prefill tiles): the only int8 workspace is the fp32 partials
+    where k is split across at least 4 workgroups (down projections here),
+    and no call writes a bf16 copy of its weights. Across the routes (the
+    streaming kernel for K % 64 != 0, the split-K tiles, the split across
+    workgroups, the prefill tiles and gemm_kernel, ragged shapes) the result
+    matches the dequantise-then-matmul oracle, and where nothing splits the
+    call through the C ABI without a workspace gives the same bits."""
+    import ctypes
+
     from llms_amd import _lib
 
     gu = op == "gate-up"
-    assert (_lib.capi().fp_workspace_bytes_w8(M, N, K, int(gu)) > 0) == dq
+    lib = _lib.capi()
+    assert (lib.fp_workspace_bytes_w8(M, N, K, int(gu)) > 0) == split
     kern = _kernels()
     rows = _rows(M, limit=64)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     if gu:
         x, wg, wu = ffn_inputs(170 + M, M, K, N)
         qg, sg = _quant(wg)
         qu, su = _quant(wu)
-        y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+        xd = x.to(DEV)
+        yd = kern.fused_gate_up_silu_w8(xd, qg, sg, qu, su)
         out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
                                            qu.cpu().numpy(), su.cpu().numpy())
+        yr = torch.empty_like(yd)
+        assert lib.fp_gate_up_silu_w8(xd.data_ptr(), K, qg.data_ptr(), K, sg.data_ptr(),
+                                      qu.data_ptr(), K, su.data_ptr(), yr.data_ptr(), N, M, N, K,
+                                      st) == 0
     else:
         x, w = qkv_inputs(180 + M, M, K, N, 0)
         q, s = _quant(w)
+        xd = x.to(DEV)
+        n_k = N // 6 if op == "qkv" else 0
         if op == "qkv":
-            n_k = N // 6
-            y = torch.cat(kern.fused_qkv_w8(x.to(DEV), q, s, n_q=N - 2 * n_k, n_k=n_k), dim=-1).cpu()
+            yd = torch.cat(kern.fused_qkv_w8(xd, q, s, n_q=N - 2 * n_k, n_k=n_k), dim=-1)
         else:
-            y = kern.fused_linear_w8(x.to(DEV), q, s).cpu()
+            yd = kern.fused_linear_w8(xd, q, s)
         out = ref.ref_linear_w8(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy())
-    _check(y[rows], out, f"int8 {op} M={M} K={K} N={N}")
+        yr = torch.empty_like(yd)
+        assert lib.fp_qkv_w8(xd.data_ptr(), K, q.data_ptr(), K, s.data_ptr(), yr.data_ptr(), N, M,
+                             N - 2 * n_k, n_k, K, st) == 0
+    torch.cuda.synchronize()
+    _check(yd.cpu()[rows], out, f"int8 {op} M={M} K={K} N={N}")
+    if not split:
+        assert torch.equal(yd.view(torch.int16), yr.view(torch.int16)), f"int8 {op} M={M} no-ws bits"
+    else:
+        _check(yr.cpu()[rows], out, f"int8 {op} M={M} K={K} N={N} unsplit")
+
+
+@pytest.mark.parametrize("cell", ["4b-gate-up-2048", "8b-qkv-4096", "8b-gate-up-4096"])
+def test_int8_prefill_cells_equal_bf16_on_dequantised(cell):
+    """BASELINE's int8 prefill cells run in registers (no workspace) and
+    contract every output over the same k-steps in the same order as the
+    bf16 call, so the whole output equals the bf16 call on bf16(q * s) bit
+    for bit; a row subset also against the oracle."""
+    from llms_amd import _lib
+
+    kern = _kernels()
+    if cell == "8b-qkv-4096":
+        K, n_q, n_k, _ = QWEN3_8B
+        M, N = 4096, n_q + 2 * n_k
+        x, w = qkv_inputs(230, M, K, n_q, n_k)
+        q, s = kern.quantize_w8_per_row(w.to(DEV))
+        assert _lib.capi().fp_workspace_bytes_w8(M, N, K, 0) == 0
+        xd = x.to(DEV)
+        y = torch.cat(kern.fused_qkv_w8(xd, q, s, n_q=n_q, n_k=n_k), dim=-1)
+        yb = torch.cat(kern.triton_fused_qkv(xd, kern.dequantize_w8(q, s), n_q=n_q, n_k=n_k), dim=-1)
+        rows = _rows(M, limit=24)
+        out = ref.ref_qkv_w8_full(bits(x)[rows], q.cpu().numpy(), s.cpu().numpy(), n_q, n_k)
+    else:
+        K, _, _, N = QWEN3_8B if cell.startswith("8b") else QWEN3_4B
+        M = 4096 if cell.startswith("8b") else 2048
+        x, wg, wu = ffn_inputs(240, M, K, N)
+        qg, sg = kern.quantize_w8_per_row(wg.to(DEV))
+        qu, su = kern.quantize_w8_per_row(wu.to(DEV))
+        del wg, wu
+        assert _lib.capi().fp_workspace_bytes_w8(M, N, K, 1) == 0
+        xd = x.to(DEV)
+        y = kern.fused_gate_up_silu_w8(xd, qg, sg, qu, su)
+        yb = kern.triton_fused_gate_up_silu(xd, kern.dequantize_w8(qg, sg), kern.dequantize_w8(qu, su))
+        rows = _rows(M, limit=24)
+        out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                           qu.cpu().numpy(), su.cpu().numpy())
+    assert torch.equal(y.view(torch.int16), yb.view(torch.int16)), cell
+    _check(y.cpu()[rows], out, f"int8 {cell}")
 
 
 @pytest.mark.parametrize("M,K,N,op", [(128, 9728, 2560, "linear"), (256, 4096, 6144, "qkv"),
