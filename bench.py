@@ -234,42 +234,57 @@ def cpu_baseline(torch, stacks: dict, reps: int) -> dict:
     }
 
 
-def clock_under_load(torch, graph, replays: int = 8) -> dict:
-    """The shader clock while `graph` runs: the graph is replayed `replays`
-    times on the current stream while a second stream (default priority)
-    runs two one-thread spins back to back (torch.cuda._sleep: a fixed
-    number of shader cycles by clock64, i.e. s_memtime). HIP events on that
-    stream bracket the second spin, so the first absorbs any delay before the
-    side stream's work starts. GHz = cycles / elapsed time. The spin is one
-    wave on one CU; the replays leave room for it (one workgroup per CU).
-    The same measurement after the replays drain gives the clock of the spin
-    alone."""
-    side = torch.cuda.Stream()
-    cycles = 8_000_000
+def clock_under_load(torch, graph, seconds: float = 0.3) -> dict:
+    """The graphics clock while `graph` runs: the graph is replayed for about
+    `seconds` while a host thread samples amdsmi's GPU metrics
+    (current_gfxclks, one value per XCD) every ~2 ms; the reported figure is
+    the median over the samples of the middle 80% of the window (the mean of
+    the XCDs in each sample). None when amdsmi is not available."""
+    import threading
 
-    def spins():
-        e1 = torch.cuda.Event(enable_timing=True)
-        e2 = torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(side):
-            torch.cuda._sleep(cycles // 4)
-            e1.record()
-            torch.cuda._sleep(cycles)
-            e2.record()
-        return e1, e2
+    try:
+        import amdsmi
 
-    for _ in range(replays):
+        amdsmi.amdsmi_init()
+        handles = amdsmi.amdsmi_get_processor_handles()
+        h = handles[torch.cuda.current_device()] if len(handles) > 1 else handles[0]
+    except Exception as e:  # noqa: BLE001 - report, do not fail the bench
+        return {"ghz_under_load": None, "method": f"amdsmi unavailable ({type(e).__name__})"}
+
+    def sample():
+        m = amdsmi.amdsmi_get_gpu_metrics_info(h)
+        v = m.get("current_gfxclks")
+        vals = [float(c) for c in (v if isinstance(v, list) else [m.get("current_gfxclk")])
+                if isinstance(c, (int, float)) and 0 < c < 10000]
+        return sum(vals) / len(vals) if vals else None
+
+    once = time_graph(torch, graph, 1, 1)
+    reps = max(4, int(seconds / max(once, 1e-6)))
+    samples, stop = [], threading.Event()
+
+    def poll():
+        while not stop.is_set():
+            try:
+                c = sample()
+            except Exception:  # noqa: BLE001
+                c = None
+            if c:
+                samples.append(c)
+            time.sleep(0.002)
+
+    for _ in range(reps):
         graph.replay()
-    e1, e2 = spins()
+    t = threading.Thread(target=poll)
+    t.start()
     torch.cuda.synchronize()
-    loaded = cycles / (e1.elapsed_time(e2) / 1e3) / 1e9
-    e1, e2 = spins()
-    torch.cuda.synchronize()
-    idle = cycles / (e1.elapsed_time(e2) / 1e3) / 1e9
-    ok = 0.3 < loaded < 3.5
-    return {"ghz_under_load": round(loaded, 3) if ok else None,
-            "ghz_spin_alone": round(idle, 3) if 0.3 < idle < 3.5 else None,
-            "method": "torch.cuda._sleep (s_memtime cycles) on a side stream during the "
-                      "prefill graph replays, HIP events around the second of two spins"}
+    stop.set()
+    t.join()
+    n = len(samples)
+    mid = sorted(samples[n // 10: n - n // 10]) if n >= 10 else sorted(samples)
+    mhz = mid[len(mid) // 2] if mid else None
+    return {"ghz_under_load": round(mhz / 1e3, 3) if mhz else None, "samples": n,
+            "method": "amdsmi current_gfxclks (mean of the XCDs) sampled every ~2 ms during "
+                      f"{reps} prefill graph replays, median of the middle 80%"}
 
 
 def counters_run(torch, kern, shape, layers: int, Mp: int = 2048, blt: bool = False) -> dict:
@@ -324,7 +339,7 @@ def counters_run(torch, kern, shape, layers: int, Mp: int = 2048, blt: bool = Fa
     }
 
 
-def decode_run(torch, n_tok: int) -> dict:
+def decode_run(torch, n_tok: int, fused_only: bool = False) -> dict:
     """Greedy decode of n_tok tokens after a 128-token prefill on a Qwen3-4B-
     shaped decoder (``llms_amd.harness``, random weights): the reference's
     eager modules (hipBLASLt ``F.linear``, torch RMSNorm), then the same model
@@ -380,16 +395,106 @@ def decode_run(torch, n_tok: int) -> dict:
 
     out = {"mode": "decode", "model": "qwen3-4b shapes, random weights", "prompt": P,
            "tokens": n_tok, "ms_per_token": {}, "verify_ms_per_step": {}}
-    out["ms_per_token"]["reference_eager"] = round(eager_ms(), 3)
-    out["ms_per_token"]["reference_graph"] = round(graph_ms(1), 3)
-    log("decode: reference path timed; swapping in the fused modules")
+    if not fused_only:
+        out["ms_per_token"]["reference_eager"] = round(eager_ms(), 3)
+        out["ms_per_token"]["reference_graph"] = round(graph_ms(1), 3)
+        log("decode: reference path timed; swapping in the fused modules")
     apply_triton_kernels(m, fuse_norm=True, linear_down_o=True)
+    if fused_only:
+        # only the graph-replayed fused decode step (for a kernel trace of it)
+        out["ms_per_token"]["fused_graph"] = round(graph_ms(1), 3)
+        out["tokens_per_s"] = {k: round(1e3 / v, 1) for k, v in out["ms_per_token"].items()}
+        return out
     out["ms_per_token"]["fused_eager"] = round(eager_ms(), 3)
     out["ms_per_token"]["fused_graph"] = round(graph_ms(1), 3)
     for T in (4, 8):
         out["verify_ms_per_step"][f"fused_graph_T{T}"] = round(graph_ms(T), 3)
     out["tokens_per_s"] = {k: round(1e3 / v, 1) for k, v in out["ms_per_token"].items()}
     return out
+
+
+def launch_gap_run(torch, kern, reps: int) -> dict:
+    """What a decode launch costs besides its bytes (Qwen3-4B, M = 1, graph
+    replay): the gap between dependent kernels of a graph (72 one-element
+    torch additions per replay, the same count as the decode step's
+    launches); the 72-launch decode step over 36 distinct layer weight sets
+    (the headline workload) and over one weight set reused by every layer
+    (131 MB, within the 256 MB Infinity Cache); and the two fused launches
+    alone on 36 sets. One JSON line."""
+    K, n_q, n_k, inter = SHAPES["qwen3-4b"]
+    n_qkv = n_q + 2 * n_k
+    out = {"mode": "launch_gap", "shape": "qwen3-4b", "M": 1}
+    z = torch.zeros(1, device="cuda")
+    g = capture(torch, lambda: [z.add_(1.0) for _ in range(72)])
+    out["tiny_kernel_us"] = round(time_graph(torch, g, reps, 200) / 72 * 1e6, 3)
+    del g
+    st = Stack(torch, SHAPES["qwen3-4b"], 36, M=1)
+    for name, layer in (("step_36_sets", lambda l: l), ("step_1_set", lambda l: 0)):
+        g = capture(torch, lambda: [
+            (kern.triton_fused_qkv(st.x_attn, st.wqkv[layer(l)], n_q=n_q, n_k=n_k),
+             kern.triton_fused_gate_up_silu(st.x_ffn, st.wg[layer(l)], st.wu[layer(l)]))
+            for l in range(36)])
+        sec = time_graph(torch, g, reps, warm_replays(torch, g, 20))
+        out[f"{name}_us"] = round(sec * 1e6, 1)
+        out[f"{name}_gbs"] = round(36 * pair_bytes(1, K, n_qkv, inter) / sec / 1e9, 1)
+        del g
+    out["gate_up_us"] = round(kernel_seconds(torch, [
+        lambda l=l: kern.triton_fused_gate_up_silu(st.x_ffn, st.wg[l], st.wu[l]) for l in range(36)],
+        reps) * 1e6, 3)
+    out["qkv_us"] = round(kernel_seconds(torch, [
+        lambda l=l: kern.triton_fused_qkv(st.x_attn, st.wqkv[l], n_q=n_q, n_k=n_k) for l in range(36)],
+        reps) * 1e6, 3)
+    # what the step would take with no gap: 72 launches' worth of gaps removed
+    out["step_minus_gaps_us"] = round(out["step_36_sets_us"] - 72 * out["tiny_kernel_us"], 1)
+    return out
+
+
+NORM_M = (1, 2, 8, 64, 512)
+
+
+def norm_run(torch, kern, reps: int) -> dict:
+    """The RMSNorm prologue fused into the projections (Qwen3-4B QKV and
+    gate-up, bf16): per M in NORM_M, the fused call (fused_rmsnorm_qkv /
+    fused_rmsnorm_gate_up_silu: one launch in the row-streaming regime, M <=
+    2; else the norm kernel, then the projection) against the eager pair the
+    engine runs (the reference's RMSNorm module restated in
+    llms_amd.kernels._eager, then the fused projection) and the projection
+    alone. Graph replay over cycled weight sets (36 up to 64 rows, 4 at 512),
+    average per call. One JSON line per M."""
+    from llms_amd.kernels import fused_norm as fn
+    from llms_amd.kernels._eager import RMSNorm
+
+    K, n_q, n_k, inter = SHAPES["qwen3-4b"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    norm = RMSNorm(K).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(1.0 + 0.1 * torch.randn(K, generator=g, device="cuda"))
+    gamma = norm.weight.detach()
+    for M in NORM_M:
+        L = 36 if M <= 64 else 4
+        st = Stack(torch, SHAPES["qwen3-4b"], L, M, seed=M)
+        out = {"mode": "norm", "M": M, "weight_sets": L}
+        with torch.no_grad():
+            cases = {
+                "qkv_fused": lambda l: fn.fused_rmsnorm_qkv(st.x_attn, gamma, norm.eps, st.wqkv[l],
+                                                            n_q=n_q, n_k=n_k),
+                "qkv_norm_then_qkv": lambda l: kern.triton_fused_qkv(norm(st.x_attn), st.wqkv[l],
+                                                                     n_q=n_q, n_k=n_k),
+                "qkv_alone": lambda l: kern.triton_fused_qkv(st.x_attn, st.wqkv[l], n_q=n_q, n_k=n_k),
+                "gate_up_fused": lambda l: fn.fused_rmsnorm_gate_up_silu(st.x_ffn, gamma, norm.eps,
+                                                                         st.wg[l], st.wu[l]),
+                "gate_up_norm_then_gate_up": lambda l: kern.triton_fused_gate_up_silu(
+                    norm(st.x_ffn), st.wg[l], st.wu[l]),
+                "gate_up_alone": lambda l: kern.triton_fused_gate_up_silu(st.x_ffn, st.wg[l], st.wu[l]),
+            }
+            for name, fn_l in cases.items():
+                t = kernel_seconds(torch, [lambda l=l, f=fn_l: f(l) for l in range(L)], reps)
+                out[f"{name}_us"] = round(t * 1e6, 2)
+        print(json.dumps(out), flush=True)
+        del st
+        torch.cuda.empty_cache()
+    return {"mode": "norm", "done": True}
 
 
 def linear_run(torch, kern, M: int, N: int, K: int, reps: int) -> dict:
@@ -679,6 +784,16 @@ def main() -> int:
                          "weights: reference eager path vs fused modules, eager and "
                          "graph-replayed steps; prints one JSON line")
     ap.add_argument("--decode-tokens", type=int, default=32)
+    ap.add_argument("--decode-fused", action="store_true",
+                    help="with --decode: only the graph-replayed fused decode step (for a kernel "
+                         "trace of that step)")
+    ap.add_argument("--launch-gap", action="store_true",
+                    help="the graph launch gap (72 tiny kernels) and the M = 1 decode step over "
+                         "36 weight sets and over one (cache-resident); prints one JSON line")
+    ap.add_argument("--norm", action="store_true",
+                    help="the RMSNorm prologue fused into the projections against the eager "
+                         "norm + projection, Qwen3-4B at M in 1, 2, 8, 64, 512; one JSON line "
+                         "per M")
     ap.add_argument("--configs", action="store_true",
                     help="time both projections on every BASELINE configuration (with "
                          "hipBLASLt for scale); one JSON line per configuration")
@@ -721,10 +836,16 @@ def main() -> int:
               flush=True)
         return 0
     if args.decode:
-        print(json.dumps(decode_run(torch, args.decode_tokens)), flush=True)
+        print(json.dumps(decode_run(torch, args.decode_tokens, args.decode_fused)), flush=True)
         return 0
     if args.configs:
         configs_run(torch, kern, args.steps)
+        return 0
+    if args.norm:
+        norm_run(torch, kern, args.steps)
+        return 0
+    if args.launch_gap:
+        print(json.dumps(launch_gap_run(torch, kern, args.steps)), flush=True)
         return 0
     if args.shards:
         shards_run(torch, kern, args.steps)
