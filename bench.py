@@ -600,6 +600,8 @@ PROFILE_SET = [
     ("8B M=256", "qwen3-8b", 256, False, 1),
     ("8B int8 M=64", "qwen3-8b", 64, True, 1),
     ("8B int8 M=256", "qwen3-8b", 256, True, 1),
+    ("8B M=4096", "qwen3-8b", 4096, False, 1),
+    ("8B int8 M=4096", "qwen3-8b", 4096, True, 1),
     ("prefill M=8192", "qwen3-4b", 8192, False, 1),
     ("8B TP=2 shard M=512", "qwen3-8b", 512, False, 2),
     ("8B TP=4 shard M=512", "qwen3-8b", 512, False, 4),
@@ -607,7 +609,7 @@ PROFILE_SET = [
 ]
 
 
-def profile_set_run(torch, kern, reps: int) -> dict:
+def profile_set_run(torch, kern, reps: int, only: str | None = None) -> dict:
     """A fixed sequence for rocprofv3 runs (kernel trace, --pmc passes): each
     PROFILE_SET entry over its own cycled weight sets (36 for decode-sized
     calls, else enough to pass the Infinity Cache), replayed in a HIP graph
@@ -615,6 +617,8 @@ def profile_set_run(torch, kern, reps: int) -> dict:
     measured per-launch times."""
     out = {"mode": "profile_set", "entries": []}
     for label, model, M, int8, tp in PROFILE_SET:
+        if only is not None and label != only:
+            continue
         K, n_q, n_k, inter = shard_shape(model, tp)
         n = n_q + 2 * n_k
         wbytes = (1 if int8 else 2) * K * (n + 2 * inter)
@@ -806,6 +810,8 @@ def main() -> int:
     ap.add_argument("--profile-set", action="store_true",
                     help="the fixed kernel sequence the profiles/ summaries other than the "
                          "default bench's are taken from (one JSON line per entry)")
+    ap.add_argument("--only", metavar="LABEL",
+                    help="with --profile-set: run only the entry with this label")
     ap.add_argument("--linear", metavar="M,N,K",
                     help="time only the plain projection (down / o) of this shape over "
                          "cycled weight sets and print one JSON line (profiling aid)")
@@ -851,7 +857,10 @@ def main() -> int:
         shards_run(torch, kern, args.steps)
         return 0
     if args.profile_set:
-        profile_set_run(torch, kern, args.steps)
+        if args.only is not None and args.only not in [e[0] for e in PROFILE_SET]:
+            print(f"bench.py: no profile-set entry {args.only!r}", file=sys.stderr)
+            return 2
+        profile_set_run(torch, kern, args.steps, args.only)
         return 0
     if args.ship_gate:
         print(json.dumps(ship_gate_run(torch, kern)), flush=True)
