@@ -177,7 +177,7 @@ int fp_linear_bf16_ws(const void* x, int64_t ldx,
  * workgroup into LDS); no bf16 copy of the weights is written anywhere. The
  * workspace serves only the k split across workgroups: for the shapes whose
  * plan splits k over at least 4 workgroups (fp_workspace_bytes_w8(M, N, K,
- * gate_up) > 0: down and o projections at 96-768 rows, Qwen3-8B QKV at
+ * gate_up) > 0: down and o projections at some row counts between 65 and 1792, Qwen3-8B QKV at
  * 129-256), given that much workspace, the split runs with its fp32
  * partials there. Without it those calls run unsplit, with the same
  * contract.

@@ -57,7 +57,7 @@ inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 // int8 calls always dequantise in registers (or once per workgroup into
 // LDS in the prefill tiles); no bf16 copy of the weights is ever written.
 // With a workspace, the calls whose plan splits k across at least 4
-// workgroups (gemm_split_plan: down and o at 96-512 rows, 8B QKV at 129-256)
+// workgroups (gemm_split_plan: Qwen3 down and o at row counts between 65 and 1792, 8B QKV at 129-256)
 // run that split on the int8 weights (gemm_kernel dequantising in registers,
 // fp32 partials in the workspace, the fixed-order reduce). Excluded: the
 // shapes the int8 split-K tiles take (splitk8_shape) and those the
