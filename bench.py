@@ -449,6 +449,80 @@ def launch_gap_run(torch, kern, reps: int) -> dict:
     return out
 
 
+# Row-streaming launches (M = 1) whose size is swept at a fixed grid shape:
+# (label, K, gate_up, int8, output widths). Each width is a whole number of
+# workgroups of the shape the dispatch picks (bf16: 8 waves of one row or row
+# pair; int8 with x from L2: 4 waves; K = 4096: x staged in LDS).
+LAUNCH_FIT = (
+    ("bf16 gate-up, K=2560, 8 waves x 1 row pair", 2560, True, False, (1216, 2432, 4864, 9728, 19456)),
+    ("bf16 QKV, K=2560, 8 waves x 1 row", 2560, False, False, (1536, 3072, 6144, 12288, 24576)),
+    ("int8 gate-up, K=2560, 4 waves x 1 row pair", 2560, True, True, (1216, 2432, 4864, 9728, 19456)),
+    ("bf16 gate-up, K=4096, 8 waves x 1 row pair, x in LDS", 4096, True, False, (1536, 3072, 6144, 12288)),
+)
+
+
+def launch_fit_run(torch, kern, reps: int) -> None:
+    """The fixed cost F of a row-streaming launch at a given grid shape: per
+    LAUNCH_FIT entry, the M = 1 launch over output widths that double, each
+    timed by graph replay over enough distinct weight sets (at least 1.2 GB
+    per replay, so the 256 MB Infinity Cache holds none of it between uses),
+    and the least-squares line t = F + bytes / B through the points (F in us,
+    B in TB/s). A one-element torch kernel in the same kind of graph gives
+    the launch floor of any kernel. One JSON line per entry."""
+    z = torch.zeros(1, device="cuda")
+    g = capture(torch, lambda: [z.add_(1.0) for _ in range(72)])
+    print(json.dumps({"mode": "launch_fit", "tiny_kernel_us":
+                      round(time_graph(torch, g, reps, 200) / 72 * 1e6, 3)}), flush=True)
+    del g
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    for label, K, gu, int8, widths in LAUNCH_FIT:
+        pts = []
+        x = torch.randn(1, K, generator=gen, device="cuda").to(torch.bfloat16)
+        for N in widths:
+            mats = 2 if gu else 1
+            per = mats * N * K * (1 if int8 else 2) + (mats * N * 4 if int8 else 0)
+            sets = int(min(400, max(8, -(-1_200_000_000 // per))))
+            if int8:
+                q = torch.randint(-127, 128, (sets, mats, N, K), generator=gen, device="cuda",
+                                  dtype=torch.int8)
+                s = torch.rand(sets, mats, N, generator=gen, device="cuda") * 1e-3 + 1e-4
+                if gu:
+                    fns = [lambda i=i: kern.fused_gate_up_silu_w8(x, q[i, 0], s[i, 0], q[i, 1], s[i, 1])
+                           for i in range(sets)]
+                else:
+                    fns = [lambda i=i: kern.fused_linear_w8(x, q[i, 0], s[i, 0]) for i in range(sets)]
+            else:
+                w = torch.randn(sets, mats, N, K, generator=gen, device="cuda",
+                                dtype=torch.bfloat16)
+                if gu:
+                    fns = [lambda i=i: kern.triton_fused_gate_up_silu(x, w[i, 0], w[i, 1])
+                           for i in range(sets)]
+                else:
+                    n_k = N // 6
+                    fns = [lambda i=i: kern.triton_fused_qkv(x, w[i, 0], n_q=N - 2 * n_k, n_k=n_k)
+                           for i in range(sets)]
+            t = kernel_seconds(torch, fns, reps)
+            nbytes = per + 2 * K + 2 * N
+            pts.append({"N": N, "sets": sets, "bytes": nbytes, "us": round(t * 1e6, 3)})
+            del fns
+            if int8:
+                del q, s
+            else:
+                del w
+            torch.cuda.empty_cache()
+        n = len(pts)
+        mb = sum(p["bytes"] for p in pts) / n
+        mt = sum(p["us"] for p in pts) / n
+        sxx = sum((p["bytes"] - mb) ** 2 for p in pts)
+        slope = sum((p["bytes"] - mb) * (p["us"] - mt) for p in pts) / sxx  # us per byte
+        F = mt - slope * mb
+        resid = max(abs(p["us"] - (F + slope * p["bytes"])) for p in pts)
+        print(json.dumps({"mode": "launch_fit", "shape": label, "points": pts,
+                          "F_us": round(F, 3), "B_tbs": round(1e-6 / slope, 3),
+                          "max_residual_us": round(resid, 3)}), flush=True)
+
+
 NORM_M = (1, 2, 8, 64, 512)
 
 
@@ -794,6 +868,10 @@ def main() -> int:
     ap.add_argument("--launch-gap", action="store_true",
                     help="the graph launch gap (72 tiny kernels) and the M = 1 decode step over "
                          "36 weight sets and over one (cache-resident); prints one JSON line")
+    ap.add_argument("--launch-fit", action="store_true",
+                    help="the fixed cost of a row-streaming launch at four grid shapes: M = 1 "
+                         "over doubling output widths, t = F + bytes / B fitted; one JSON line "
+                         "per shape")
     ap.add_argument("--norm", action="store_true",
                     help="the RMSNorm prologue fused into the projections against the eager "
                          "norm + projection, Qwen3-4B at M in 1, 2, 8, 64, 512; one JSON line "
@@ -852,6 +930,9 @@ def main() -> int:
         return 0
     if args.launch_gap:
         print(json.dumps(launch_gap_run(torch, kern, args.steps)), flush=True)
+        return 0
+    if args.launch_fit:
+        launch_fit_run(torch, kern, args.steps)
         return 0
     if args.shards:
         shards_run(torch, kern, args.steps)
