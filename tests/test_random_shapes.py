@@ -1,0 +1,133 @@
+"""Seeded random shapes across every dispatch regime, against the oracle.
+
+The targeted GPU tests pin each kernel family at the shapes that select it.
+This file draws shapes at random (fixed seed) so that the planner's
+boundaries are crossed at places nobody picked: row counts from 1 to a few
+thousand (the row-streaming, streaming, split-K, staged, tiled and
+persistent-tile regimes, with and without the k split across workgroups),
+K aligned to 64 or 128, aligned to 8 only, or ragged, and output widths that
+leave partial tiles. Each shape runs the bf16 QKV, gate-up-SiLU and plain
+projections and their int8 weight-only forms through the Python surface
+(which passes the split workspace the torch ops allocate), and is checked
+against the oracle on up to 48 rows (``oracle.ref.check_parity``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ref
+from tests._util import bits, ffn_inputs, qkv_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+SPECIAL_M = (1, 2, 3, 5, 8, 9, 16, 17, 48, 63, 64, 65, 96, 128, 129, 255, 256, 257, 511, 512,
+             513, 1023, 1536, 2048, 2049)
+
+
+def _shapes(n: int, seed: int = 2024):
+    """(M, K, n_q, n_k, I): M log-uniform in [1, 3000] or a regime edge; K a
+    multiple of 64 (60%), of 8 only (25%) or anything (15%), at most 5120;
+    output widths with partial tiles, N x K at most 1.6e7 (oracle time)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        if i % 2 == 0:
+            M = int(rng.choice(SPECIAL_M))
+        else:
+            M = int(np.exp(rng.uniform(0, np.log(3000))))
+        u = rng.uniform()
+        if u < 0.6:
+            K = 64 * int(rng.integers(1, 81))
+        elif u < 0.85:
+            K = 8 * int(rng.integers(1, 641))
+        else:
+            K = int(rng.integers(1, 5121))
+        nmax = max(16, int(1.6e7 // K))
+        n_k = int(rng.integers(1, max(2, min(1024, nmax // 6)) + 1))
+        n_q = int(rng.integers(1, max(2, min(4096, nmax - 2 * n_k)) + 1))
+        inter = int(rng.integers(1, max(2, min(12288, nmax // 2)) + 1))
+        out.append((M, K, n_q, n_k, inter))
+    return out
+
+
+SHAPES = _shapes(64)
+
+
+def _kernels():
+    from llms_amd import kernels
+
+    return kernels
+
+
+def _rows(M: int, seed: int) -> np.ndarray:
+    if M <= 48:
+        return np.arange(M)
+    r = np.random.default_rng(seed).choice(M, size=46, replace=False)
+    return np.sort(np.concatenate([r, [0, M - 1]]))
+
+
+def _check(y: torch.Tensor, out: ref.OracleOut, label: str) -> None:
+    p = ref.check_parity(bits(y), out)
+    print(f"{label}: {p}")
+    assert p.ok, f"{label}: {p}"
+
+
+def _quant(w: torch.Tensor):
+    q, s = _kernels().quantize_w8_per_row(w.to(DEV))
+    qo, so = ref.quantize_w8_per_row(bits(w))
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy(), so)
+    return q, s
+
+
+@pytest.mark.parametrize("i", range(len(SHAPES)))
+def test_random_shape(i):
+    M, K, n_q, n_k, inter = SHAPES[i]
+    kern = _kernels()
+    tag = f"case {i}: M={M} K={K} n_q={n_q} n_k={n_k} I={inter}"
+    rows = _rows(M, i)
+
+    x, w = qkv_inputs(5000 + i, M, K, n_q, n_k)
+    q, k, v = kern.triton_fused_qkv(x.to(DEV), w.to(DEV), n_q=n_q, n_k=n_k)
+    y = torch.cat([q, k, v], -1).cpu()
+    _check(y[rows], ref.ref_qkv_full(bits(x)[rows], bits(w), n_q, n_k), f"{tag} qkv")
+
+    # the plain projection on the same operands (one column block)
+    y = kern.fused_linear(x.to(DEV), w.to(DEV)).cpu()
+    _check(y[rows], ref.ref_linear(bits(x)[rows], bits(w)), f"{tag} linear")
+
+    qw, sw = _quant(w)
+    q, k, v = kern.fused_qkv_w8(x.to(DEV), qw, sw, n_q=n_q, n_k=n_k)
+    y = torch.cat([q, k, v], -1).cpu()
+    out = ref.ref_qkv_w8_full(bits(x)[rows], qw.cpu().numpy(), sw.cpu().numpy(), n_q, n_k)
+    _check(y[rows], out, f"{tag} int8 qkv")
+
+    y = kern.fused_linear_w8(x.to(DEV), qw, sw).cpu()
+    out = ref.ref_linear_w8(bits(x)[rows], qw.cpu().numpy(), sw.cpu().numpy())
+    _check(y[rows], out, f"{tag} int8 linear")
+
+    x, wg, wu = ffn_inputs(6000 + i, M, K, inter)
+    y = kern.triton_fused_gate_up_silu(x.to(DEV), wg.to(DEV), wu.to(DEV)).cpu()
+    _check(y[rows], ref.ref_gate_up_silu_full(bits(x)[rows], bits(wg), bits(wu)), f"{tag} gate-up")
+
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+    out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
+                                       qu.cpu().numpy(), su.cpu().numpy())
+    _check(y[rows], out, f"{tag} int8 gate-up")
+
+
+def test_shapes_cover_the_regimes():
+    """No GPU needed for the draw itself, but it lives with the GPU cases:
+    the seeded shapes must reach every regime the test claims."""
+    Ms = [s[0] for s in SHAPES]
+    Ks = [s[1] for s in SHAPES]
+    assert min(Ms) <= 2 and any(3 <= m <= 8 for m in Ms) and any(9 <= m <= 64 for m in Ms)
+    assert any(65 <= m <= 256 for m in Ms) and any(m >= 512 for m in Ms)
+    assert any(k % 64 == 0 for k in Ks) and any(k % 64 != 0 and k % 8 == 0 for k in Ks)
+    assert any(k % 8 != 0 for k in Ks)
