@@ -6,10 +6,11 @@ boundaries are crossed at places nobody picked: row counts from 1 to a few
 thousand (the row-streaming, streaming, split-K, staged, tiled and
 persistent-tile regimes, with and without the k split across workgroups),
 K aligned to 64 or 128, aligned to 8 only, or ragged, and output widths that
-leave partial tiles. Each shape runs the bf16 QKV, gate-up-SiLU and plain
-projections and their int8 weight-only forms through the Python surface
-(which passes the split workspace the torch ops allocate), and is checked
-against the oracle on up to 48 rows (``oracle.ref.check_parity``).
+leave partial tiles; every third case passes x as a row-strided view. Each
+shape runs the bf16 QKV, gate-up-SiLU and plain projections and their int8
+weight-only forms through the Python surface (which passes the split
+workspace the torch ops allocate), and is checked against the oracle on up
+to 48 rows (``oracle.ref.check_parity``).
 """
 
 from __future__ import annotations
@@ -76,6 +77,17 @@ def _check(y: torch.Tensor, out: ref.OracleOut, label: str) -> None:
     assert p.ok, f"{label}: {p}"
 
 
+def _on_device(x: torch.Tensor, i: int) -> torch.Tensor:
+    """x on the device; every third case as a row-strided view (row stride K
+    plus 1-24 elements, unit inner stride), as a slice of a wider buffer."""
+    if i % 3 != 1:
+        return x.to(DEV)
+    pad = 1 + (i * 7) % 24
+    full = torch.zeros(x.shape[0], x.shape[1] + pad, dtype=x.dtype)
+    full[:, : x.shape[1]] = x
+    return full.to(DEV)[:, : x.shape[1]]
+
+
 def _quant(w: torch.Tensor):
     q, s = _kernels().quantize_w8_per_row(w.to(DEV))
     qo, so = ref.quantize_w8_per_row(bits(w))
@@ -92,31 +104,33 @@ def test_random_shape(i):
     rows = _rows(M, i)
 
     x, w = qkv_inputs(5000 + i, M, K, n_q, n_k)
-    q, k, v = kern.triton_fused_qkv(x.to(DEV), w.to(DEV), n_q=n_q, n_k=n_k)
+    xd = _on_device(x, i)
+    q, k, v = kern.triton_fused_qkv(xd, w.to(DEV), n_q=n_q, n_k=n_k)
     y = torch.cat([q, k, v], -1).cpu()
     _check(y[rows], ref.ref_qkv_full(bits(x)[rows], bits(w), n_q, n_k), f"{tag} qkv")
 
     # the plain projection on the same operands (one column block)
-    y = kern.fused_linear(x.to(DEV), w.to(DEV)).cpu()
+    y = kern.fused_linear(xd, w.to(DEV)).cpu()
     _check(y[rows], ref.ref_linear(bits(x)[rows], bits(w)), f"{tag} linear")
 
     qw, sw = _quant(w)
-    q, k, v = kern.fused_qkv_w8(x.to(DEV), qw, sw, n_q=n_q, n_k=n_k)
+    q, k, v = kern.fused_qkv_w8(xd, qw, sw, n_q=n_q, n_k=n_k)
     y = torch.cat([q, k, v], -1).cpu()
     out = ref.ref_qkv_w8_full(bits(x)[rows], qw.cpu().numpy(), sw.cpu().numpy(), n_q, n_k)
     _check(y[rows], out, f"{tag} int8 qkv")
 
-    y = kern.fused_linear_w8(x.to(DEV), qw, sw).cpu()
+    y = kern.fused_linear_w8(xd, qw, sw).cpu()
     out = ref.ref_linear_w8(bits(x)[rows], qw.cpu().numpy(), sw.cpu().numpy())
     _check(y[rows], out, f"{tag} int8 linear")
 
     x, wg, wu = ffn_inputs(6000 + i, M, K, inter)
-    y = kern.triton_fused_gate_up_silu(x.to(DEV), wg.to(DEV), wu.to(DEV)).cpu()
+    xd = _on_device(x, i)
+    y = kern.triton_fused_gate_up_silu(xd, wg.to(DEV), wu.to(DEV)).cpu()
     _check(y[rows], ref.ref_gate_up_silu_full(bits(x)[rows], bits(wg), bits(wu)), f"{tag} gate-up")
 
     qg, sg = _quant(wg)
     qu, su = _quant(wu)
-    y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+    y = kern.fused_gate_up_silu_w8(xd, qg, sg, qu, su).cpu()
     out = ref.ref_gate_up_silu_w8_full(bits(x)[rows], qg.cpu().numpy(), sg.cpu().numpy(),
                                        qu.cpu().numpy(), su.cpu().numpy())
     _check(y[rows], out, f"{tag} int8 gate-up")
