@@ -138,6 +138,9 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
 __device__ __forceinline__ u32x4 ld16_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
+__device__ __forceinline__ u32x2 ld8_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+}
 
 // Eight bf16 starting at element k of a row of length K, zero beyond K.
 // ALIGNED: the row base is 16-byte aligned and K % 8 == 0, so a chunk of eight

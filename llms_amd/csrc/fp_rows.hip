@@ -247,6 +247,84 @@ __global__ __launch_bounds__(NW * kWave) void rows_kernel(StreamArgs a) {
   }
 }
 
+
+// int8 gate-up at one x row without a fused norm: each wave owns one row pair
+// of Wg and Wu and reads it 8 bytes per lane per chunk (512 k per wave
+// instruction, one MFMA per chunk and matrix), so that K = 2560 fills five
+// chunks exactly instead of leaving half of a third 1024-k chunk empty, with
+// the whole row pair in flight (U chunks). x comes from L2 chunk by chunk
+// (XG, K <= 2560) or is staged once per workgroup in LDS. The dot products
+// and the epilogue are those of rows_kernel (MFMA diagonal, fixed-order wave
+// sum, torch's rounding points); the dequantisation is the exact
+// dequant8_bf16.
+template <int NW, int U, bool XG>
+__global__ __launch_bounds__(NW * kWave) void rows_gate_up_w8_kernel(StreamArgs a) {
+  constexpr int KC = 512, KL = 8;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int64_t K = a.K;
+  const int J = (int)((K + KC - 1) / KC);  // chunks per row
+  const int64_t row = (int64_t)blockIdx.x * NW + wave;
+  const int T = row < a.N ? J : 0;          // chunks of this wave
+  const int8_t* g = (const int8_t*)a.w0 + (row < a.N ? row : 0) * a.ldw0;
+  const int8_t* u = (const int8_t*)a.w1 + (row < a.N ? row : 0) * a.ldw1;
+
+  // chunk t sits in slot t % U; zero past the row's end
+  u32x2 wg[U], wu[U];
+  u32x4 xg[XG ? U : 1];
+  int ij = 0;
+  auto issue = [&](int s) {
+    if (ij < T) {
+      const int64_t k = (int64_t)ij * KC + KL * lane;
+      if constexpr (XG) xg[s] = load_bf16x8<true>(a.x, k, K);
+      if (k < K) {
+        wg[s] = ld8_nt(g + k);
+        wu[s] = ld8_nt(u + k);
+      } else {
+        wg[s] = u32x2{0u, 0u};
+        wu[s] = u32x2{0u, 0u};
+      }
+      ++ij;
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < U; ++s) issue(s);
+  if constexpr (!XG) {
+    // x[0, 0:K] -> LDS, zero beyond K, while the first weight loads fly
+    const int64_t nvec = (int64_t)J * KC / 8;
+    for (int64_t i = threadIdx.x; i < nvec; i += NW * kWave)
+      *reinterpret_cast<u32x4*>(xs + i * 8) = load_bf16x8<true>(a.x, i * 8, K);
+    __syncthreads();
+  }
+  float sg = 0.f, su = 0.f;
+  if (T > 0) {
+    sg = a.s0[row];
+    su = a.s1[row];
+  }
+  const float ng = -128.f * sg, nu = -128.f * su;
+  f32x4 dg = {0.f, 0.f, 0.f, 0.f}, du = dg;
+  for (int t0 = 0; t0 < T; t0 += U) {
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      const int t = t0 + s;
+      if (t < T) {
+        u32x4 xv;
+        if constexpr (XG) xv = xg[s];
+        else xv = *reinterpret_cast<const u32x4*>(xs + (int64_t)t * KC + KL * lane);
+        dg = mfma16(dequant8_bf16(wg[s].x, wg[s].y, sg, ng), xv, dg);
+        du = mfma16(dequant8_bf16(wu[s].x, wu[s].y, su, nu), xv, du);
+        issue(s);
+      }
+    }
+  }
+  if (T > 0) {
+    const float gs = wave_sum(diag(dg, lane));
+    const float us = wave_sum(diag(du, lane));
+    if (lane == 0) a.y[row] = (uint16_t)gate_up_silu_bits(gs, us);
+  }
+}
+
 // x rows staged per workgroup: M rounded up to 1, 2 or 4
 inline int64_t rows_mm(int64_t M) { return M <= 2 ? M : 4; }
 
@@ -340,6 +418,22 @@ template bool rows_supported<true>(const StreamArgs&, bool);
 // 3..4; x rows rounded up to 1, 2, 4.
 template <int MM, bool GATEUP, bool W8>
 int launch_rows_m(const StreamArgs& a, hipStream_t s) {
+  if constexpr (W8 && GATEUP && MM == 1) {
+    // int8 gate-up at one x row: 8-byte chunks, 4 waves, 5 chunks in flight
+    // (one box, µs, against the 16-byte chunks of rows_kernel: 4B 11.87-12.07
+    // -> 10.91-11.00, 8B 19.71-20.23 -> 18.89-19.89; for QKV they measured
+    // even or slower)
+    if (!a.gamma) {
+      const dim3 grid((unsigned)((a.N + 3) / 4)), block(4 * kWave);
+      if (a.K <= 2560) {
+        hipLaunchKernelGGL((rows_gate_up_w8_kernel<4, 5, true>), grid, block, 0, s, a);
+      } else {
+        const size_t shm = (size_t)((a.K + 511) / 512) * 512 * 2;
+        hipLaunchKernelGGL((rows_gate_up_w8_kernel<4, 5, false>), grid, block, shm, s, a);
+      }
+      return (int)hipGetLastError();
+    }
+  }
   if constexpr (W8) {
     if constexpr (MM == 1)
       if (!a.gamma && a.K <= 2560) return launch_rows_cfg<4, 1, 3, 1, GATEUP, true>(a, s);
