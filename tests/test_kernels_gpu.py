@@ -553,6 +553,30 @@ def test_int8_dequant_bit_exact(M):
     np.testing.assert_array_equal(y, deq[:, ks].T)
 
 
+@pytest.mark.parametrize("K", [1040, 2560, 4096, 4112])
+def test_int8_gate_up_one_row_bit_exact(K):
+    """int8 gate-up at one x row runs the 8-byte-chunk row kernel (x from L2
+    up to K = 2560, staged in LDS above; 1040 and 4112 leave a partial last
+    512-k chunk). With one-hot x each output is silu(g) * u of single
+    dequantised weights, so the kernel must equal the oracle's exact rounding
+    bit for bit; with random x it must pass the parity bar."""
+    kern = _kernels()
+    N = 100
+    x, wg, wu = ffn_inputs(880 + K, 1, K, N, w_std=0.05)
+    wg[7] = 0  # an all-zero row: s = 0, q = 0
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    args = (qg.cpu().numpy(), sg.cpu().numpy(), qu.cpu().numpy(), su.cpu().numpy())
+    y = kern.fused_gate_up_silu_w8(x.to(DEV), qg, sg, qu, su).cpu()
+    _check(y, ref.ref_gate_up_silu_w8_full(bits(x), *args), f"int8 gate-up M=1 K={K}")
+    k = int(np.random.default_rng(K).integers(K))
+    x1 = torch.zeros(1, K, dtype=torch.bfloat16)
+    x1[0, k] = 1.0
+    y = kern.fused_gate_up_silu_w8(x1.to(DEV), qg, sg, qu, su).cpu()
+    p = _check(y, ref.ref_gate_up_silu_w8_full(bits(x1), *args), f"int8 gate-up one-hot K={K}")
+    assert p.n_differ == 0, p
+
+
 @pytest.mark.parametrize("M", [2, 3, 16, 33, 64, 100, 128])
 def test_int8_split_k_tiles(M):
     """The int8 split-K tiles (weights land in LDS as int8, each lane
