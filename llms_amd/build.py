@@ -31,7 +31,7 @@ CAPI_SO = PKG / "libllms_amd_fp.so"
 TORCH_OPS_SO = PKG / "_torch_ops.so"
 
 HIP_SOURCES = ["fp_api.hip", "fp_stream.hip", "fp_rows.hip", "fp_splitk.hip", "fp_tiled.hip",
-               "fp_gemm.hip", "fp_scratch.hip"]
+               "fp_gemm.hip", "fp_scratch.hip", "fp_xpanel.hip"]
 HIP_HEADERS = ["fp_common.h", "fp_launch.h"]
 
 # gfx950 only. Packed-fp32 VALU ops (v_pk_*_f32) are disabled for all device

@@ -103,6 +103,18 @@ inline bool gemm8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
 template <bool GATEUP, bool W8>
 int launch_splitk(const StreamArgs& a, hipStream_t s);
 
+// int8 calls at spec-verify row counts that run fp_xpanel.hip (x staged once
+// per workgroup, every weight load of a wave in flight at once): 2 to 16
+// rows, K from 2048 to 2560 in whole 64-wide steps, at least 4096 outputs
+// (measured on Qwen3-4B QKV and gate-up; with K = 4096 and with bf16 weights
+// the split-K tiles stay faster). Needs splitk_supported() as well.
+inline bool xpanel8_shape(int64_t M, int64_t N, int64_t K, bool gateup) {
+  (void)gateup;
+  return M >= 2 && M <= 16 && K % 64 == 0 && K >= 2048 && K <= 2560 && N >= 4096;
+}
+template <bool GATEUP>
+int launch_xpanel8(const StreamArgs& a, hipStream_t s);
+
 // Direct-to-LDS MFMA contraction (fp_gemm.hip; int8 weights dequantised in
 // registers), used by launch_tiled when gemm_supported() holds.
 bool gemm_supported(const StreamArgs& a, bool aligned, bool w8);

@@ -349,6 +349,10 @@ int launch_stream_cfg(const StreamArgs& a, bool aligned, hipStream_t s) {
 // QKV 2 (QKV's 3x smaller grid is latency-bound and prefers occupancy).
 template <bool GATEUP, bool W8>
 int launch_stream(const StreamArgs& a, bool aligned, hipStream_t s) {
+  // int8 at 2-16 rows with K <= 2560: x staged once per workgroup, all weight
+  // loads in flight (fp_xpanel.hip)
+  if (W8 && xpanel8_shape(a.M, a.N, a.K, GATEUP) && splitk_supported(a, aligned, true))
+    return launch_xpanel8<GATEUP>(a, s);
   // int8 from a few rows: split-K tiles dequantising in registers (fp_splitk.hip)
   if (W8 && splitk8_shape(a.M, a.N, a.K, GATEUP) && splitk_supported(a, aligned, true))
     return launch_splitk<GATEUP, true>(a, s);

@@ -577,6 +577,44 @@ def test_int8_gate_up_one_row_bit_exact(K):
     assert p.n_differ == 0, p
 
 
+@pytest.mark.parametrize("M", [2, 3, 5, 8, 13, 16])
+def test_int8_verify_rows_qwen3_4b(M):
+    """int8 at 2-16 rows with K = 2560 (x staged once per workgroup, every
+    weight load in flight): Qwen3-4B-sized QKV and gate-up against the oracle,
+    with output widths that leave a partial last block of 16 rows (6150 and
+    9732) and x as a row-strided view; then one-hot x rows, whose QKV outputs
+    are single dequantised weights, y[m, n] = bf16(q[n, k_m] * s[n]), equal to
+    the oracle's dequant_w8 bit for bit."""
+    K, n_q, n_k, I = QWEN3_4B
+    kern = _kernels()
+    x, w = qkv_inputs(1300 + M, M, K, n_q + 6, n_k, w_std=0.05)
+    q, s = _quant(w)
+    full = torch.zeros(M, K + 24, dtype=torch.bfloat16)
+    full[:, :K] = x
+    xd = full.to(DEV)[:, :K]
+    yq, yk, yv = kern.fused_qkv_w8(xd, q, s, n_q=n_q + 6, n_k=n_k)
+    y = torch.cat([yq, yk, yv], -1).cpu()
+    qn, sn = q.cpu().numpy(), s.cpu().numpy()
+    _check(y, ref.ref_qkv_w8_full(bits(x), qn, sn, n_q + 6, n_k), f"int8 qkv M={M} N=6150")
+
+    ks = np.random.default_rng(M).choice(K, size=M, replace=False)
+    x1 = torch.zeros(M, K, dtype=torch.bfloat16)
+    x1[np.arange(M), ks] = 1.0
+    yq, yk, yv = kern.fused_qkv_w8(x1.to(DEV), q, s, n_q=n_q + 6, n_k=n_k)
+    np.testing.assert_array_equal(bits(torch.cat([yq, yk, yv], -1).cpu()),
+                                  ref.dequant_w8(qn, sn)[:, ks].T)
+
+    x, wg, wu = ffn_inputs(1400 + M, M, K, I + 4)
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    full[:, :K] = x
+    xd = full.to(DEV)[:, :K]
+    y = kern.fused_gate_up_silu_w8(xd, qg, sg, qu, su).cpu()
+    out = ref.ref_gate_up_silu_w8_full(bits(x), qg.cpu().numpy(), sg.cpu().numpy(),
+                                       qu.cpu().numpy(), su.cpu().numpy())
+    _check(y, out, f"int8 gate-up M={M} N=9732")
+
+
 @pytest.mark.parametrize("M", [2, 3, 16, 33, 64, 100, 128])
 def test_int8_split_k_tiles(M):
     """The int8 split-K tiles (weights land in LDS as int8, each lane
