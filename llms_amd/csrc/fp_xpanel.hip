@@ -6,10 +6,12 @@
 // the 16 Wu rows of one block of 16 outputs) over the whole of K, and all
 // the x rows (up to 16; rows past M read as zero):
 //   - x, the B operand of v_mfma_f32_16x16x32_bf16, lands in LDS by
-//     buffer_load_dwordx4 ... lds as one 2 KB plane per 64-wide k-step (16
-//     rows x 128 B, chunk c of row r at c ^ ((r >> 1) & 7), so the fragment
-//     reads of 16 rows hit distinct banks). K <= 2560 needs at most 80 KB,
-//     so two workgroups share a CU.
+//     buffer_load_dwordx4 ... lds as one plane per 64-wide k-step (XR = 16
+//     or, at up to 8 rows, 8 rows x 128 B, chunk c of row r at
+//     c ^ ((r >> 1) & 7), so the fragment reads of 16 rows hit distinct
+//     banks; with 8 staged rows, lanes of B columns 8-15 take zeros). K <=
+//     2560 needs at most 80 KB (40 KB with 8 rows), so two (four) workgroups
+//     share a CU.
 //   - Wave w contracts k-steps w, w + NW, w + 2 NW, ...; before it computes
 //     anything it issues the int8 loads of all of them (16 B per lane and
 //     row block: row li, k 16 grp .. 16 grp + 15 of the step), so the whole
@@ -31,7 +33,9 @@
 // 15.81, M = 8 17.22 -> 16.07, M = 12 18.0 -> 16.18, M = 16 18.8 -> 16.35.
 // The two libraries alternated on another box (ABBA, 3 pairs): QKV M = 3, 4,
 // 8 7.85, 7.86, 8.1 -> 7.03, 6.97, 7.08; gate-up 16.3, 16.7, 17.2 -> 15.5,
-// 15.6, 15.9. With K = 4096 (Qwen3-8B: 128 KB of x, one workgroup per CU),
+// 15.6, 15.9. Staging 8 x rows at M <= 8 (ABBA again, bit-identical): QKV M =
+// 2, 4, 8 7.1 -> 6.48-6.50, gate-up 15.6, 15.7, 16.0 -> 15.2, 15.3, 15.6. With
+// K = 4096 (Qwen3-8B: 128 KB of x, one workgroup per CU),
 // with bf16 weights, and at one row (the row kernel) the same kernel
 // measured slower.
 // Requirements (checked by the dispatcher): xpanel8_shape(), 16-byte-aligned
@@ -45,6 +49,7 @@ namespace {
 
 constexpr int kBK = 64;   // k per step
 constexpr int kNK = 40;   // k-steps the x planes hold (K <= 2560)
+constexpr int kNSW = 10;  // k-steps per wave (four waves)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -75,9 +80,10 @@ constexpr int vmcnt_imm(int v) { return (v & 15) | (7 << 4) | (15 << 8) | ((v >>
 // An offset past every buffer's range (rows past N, steps past K: zeros).
 constexpr uint32_t kPastEnd = 0x80000000u;
 
-template <int NW, int RB, int NSW, bool GATEUP>
+template <int NW, int RB, int NSW, int XR, bool GATEUP>
 __global__ __launch_bounds__(NW * kWave) void xpanel_kernel(StreamArgs a) {
-  constexpr int PL = 16 * kBK * 2;  // bytes per x plane (16 rows, one k-step)
+  constexpr int PL = XR * kBK * 2;  // bytes per x plane (XR rows, one k-step)
+  static_assert(XR == 8 || XR == 16, "8 or 16 staged x rows");
   static_assert(!GATEUP || RB % 2 == 0, "gate-up blocks come in gate/up pairs");
   static_assert(NW * NSW >= kNK, "every k-step has a wave");
   static_assert(NW * RB * 1024 <= kNK * PL, "the partial tiles fit the x planes");
@@ -89,13 +95,14 @@ __global__ __launch_bounds__(NW * kWave) void xpanel_kernel(StreamArgs a) {
   const int li = lane & 15, grp = lane >> 4;
   const int nkt = (int)(a.K / kBK);
 
-  // x rows 0..15 (past M: zero) into planes 0 .. nkt - 1, this wave's share
-  // of the 2 * nkt load instructions (8 rows each)
+  // x rows 0 .. XR - 1 (past M: zero) into planes 0 .. nkt - 1, this wave's
+  // share of the IPP * nkt load instructions (8 rows each)
+  constexpr int IPP = XR / 8;
   const int xbytes = (int)((a.M - 1) * a.ldx * 2 + a.K * 2);
-  for (int q = wave; q < 2 * nkt; q += NW) {
-    const int j = q / 2, r = (q % 2) * 8 + lane / 8;
+  for (int q = wave; q < IPP * nkt; q += NW) {
+    const int j = q / IPP, r = (q % IPP) * 8 + lane / 8;
     const uint32_t voff = (uint32_t)(r * a.ldx * 2) + (uint32_t)(((lane & 7) ^ swz(r)) * 16);
-    load_lds16(a.x, xbytes, (lds_ptr_t)(xs + j * PL + (q % 2) * 1024), voff,
+    load_lds16(a.x, xbytes, (lds_ptr_t)(xs + j * PL + (q % IPP) * 1024), voff,
                (uint32_t)(j * kBK * 2));
   }
 
@@ -136,15 +143,19 @@ __global__ __launch_bounds__(NW * kWave) void xpanel_kernel(StreamArgs a) {
   f32x4 acc[RB];
 #pragma unroll
   for (int i = 0; i < RB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int bo = swz(li);
+  // B column li reads staged row li (8 staged rows: columns 8-15 are zero)
+  const int xr = li & (XR - 1);
+  const int bo = swz(xr);
+  const bool xlive = li < XR;
 #pragma unroll
   for (int t = 0; t < NSW; ++t) {
     const int j = wave + NW * t;
     if (j >= nkt) break;  // uniform per wave
-    const char* pl = xs + j * PL + li * 128;
+    const char* pl = xs + j * PL + xr * 128;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const u32x4 b = *reinterpret_cast<const u32x4*>(pl + (((2 * grp + kk) ^ bo) * 16));
+      u32x4 b = *reinterpret_cast<const u32x4*>(pl + (((2 * grp + kk) ^ bo) * 16));
+      if constexpr (XR < 16) b = xlive ? b : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
         const u32x4 av = kk == 0 ? dequant8_bf16(wq[t][i].x, wq[t][i].y, sc[i], nsc[i])
@@ -197,15 +208,20 @@ __global__ __launch_bounds__(NW * kWave) void xpanel_kernel(StreamArgs a) {
 
 // Four waves of ten k-steps each; QKV (and plain outputs) one block of 16
 // rows per workgroup, gate-up one gate/up pair (measured against 8 waves of
-// five steps and against two QKV blocks per workgroup: even or slower).
+// five steps and against two QKV blocks per workgroup: even or slower); 8
+// staged x rows up to 8 rows, else 16.
+template <int XR, bool GATEUP>
+int launch_xpanel_cfg(const StreamArgs& a, hipStream_t s) {
+  constexpr int RB = GATEUP ? 2 : 1;
+  const int64_t rblocks = GATEUP ? 2 * ((a.N + 15) / 16) : (a.N + 15) / 16;
+  hipLaunchKernelGGL((xpanel_kernel<4, RB, kNSW, XR, GATEUP>),
+                     dim3((unsigned)((rblocks + RB - 1) / RB)), dim3(4 * kWave), 0, s, a);
+  return (int)hipGetLastError();
+}
 template <bool GATEUP>
 int launch_xpanel8(const StreamArgs& a, hipStream_t s) {
   if (a.K % kBK != 0 || a.K / kBK > kNK || a.M < 1 || a.M > 16) return (int)hipErrorInvalidValue;
-  constexpr int RB = GATEUP ? 2 : 1;
-  const int64_t rblocks = GATEUP ? 2 * ((a.N + 15) / 16) : (a.N + 15) / 16;
-  hipLaunchKernelGGL((xpanel_kernel<4, RB, 10, GATEUP>), dim3((unsigned)((rblocks + RB - 1) / RB)),
-                     dim3(4 * kWave), 0, s, a);
-  return (int)hipGetLastError();
+  return a.M <= 8 ? launch_xpanel_cfg<8, GATEUP>(a, s) : launch_xpanel_cfg<16, GATEUP>(a, s);
 }
 
 template int launch_xpanel8<false>(const StreamArgs&, hipStream_t);
