@@ -25,19 +25,15 @@
 //   - The waves' partial tiles are summed through LDS in wave order 0, 1,
 //     ... (fixed: results do not depend on scheduling); wave 0 applies the
 //     epilogue (bf16, or silu(g) * u at torch's rounding points) and stores.
-// Measured on MI355X against the split-K tiles (fp_splitk.hip; one box, µs,
-// 16 cycled weight sets): Qwen3-4B int8 QKV (2560 -> 6144) M = 2 7.03 ->
-// 6.68 (against the row kernel there), M = 3 7.93-8.22 -> 6.77, M = 4 7.93 ->
-// 6.72, M = 8 8.12 -> 7.06, M = 12 8.34 -> 7.00, M = 16 8.72 -> 7.29; gate-up
-// (2560 -> 2 x 9728) M = 2 16.28 -> 15.63, M = 3 16.39 -> 15.51, M = 4 16.8 ->
-// 15.81, M = 8 17.22 -> 16.07, M = 12 18.0 -> 16.18, M = 16 18.8 -> 16.35.
-// The two libraries alternated on another box (ABBA, 3 pairs): QKV M = 3, 4,
-// 8 7.85, 7.86, 8.1 -> 7.03, 6.97, 7.08; gate-up 16.3, 16.7, 17.2 -> 15.5,
-// 15.6, 15.9. Staging 8 x rows at M <= 8 (ABBA again, bit-identical): QKV M =
-// 2, 4, 8 7.1 -> 6.48-6.50, gate-up 15.6, 15.7, 16.0 -> 15.2, 15.3, 15.6. With
-// K = 4096 (Qwen3-8B: 128 KB of x, one workgroup per CU),
-// with bf16 weights, and at one row (the row kernel) the same kernel
-// measured slower.
+// Measured on MI355X against the split-K tiles (fp_splitk.hip), the two
+// libraries alternated on one box over 36 cycled weight sets (more than the
+// 256 MB Infinity Cache holds), µs: Qwen3-4B int8 QKV (2560 -> 6144) M = 4,
+// 8, 16 8.6, 8.9, 9.3 -> 8.2, 8.3, 8.8 (M = 2, against the row kernel: even);
+// gate-up (2560 -> 2 x 9728) M = 4 16.3 -> 15.1. Staging 8 x rows instead of
+// 16 at M <= 8 (bit-identical; gate-up over 16 sets of 100 MB): 15.5, 15.6,
+// 15.9 -> 15.2, 15.3, 15.6 at M = 3, 4, 8. With K = 4096 (Qwen3-8B: 128 KB
+// of x, one workgroup per CU), with bf16 weights, and at one row (the row
+// kernel) the same kernel measured slower.
 // Requirements (checked by the dispatcher): xpanel8_shape(), 16-byte-aligned
 // rows, operand byte sizes below 2^31, row scales present.
 #include "fp_common.h"
