@@ -116,9 +116,9 @@ def test_prefill_calls_replay_in_graph():
     a down projection split across workgroups (fp32 partials in a workspace
     from the graph's pool, then the reduce) and an int8 down projection split
     the same way, int8 QKV at 2048 rows (one round of tiles that dequantise
-    in LDS) and int8 gate-up at 2048 rows (both matrices dequantised into a
-    workspace from the graph's pool in one launch, then the bf16 tiles) —
-    replay bit-identically to the eager calls, several times, with eager work
+    in LDS) and int8 gate-up at 2048 rows (two launches of tiles that
+    dequantise once per workgroup in LDS, no workspace) — replay
+    bit-identically to the eager calls, several times, with eager work
     between the replays."""
     from llms_amd import kernels as K
     from tests._util import ffn_inputs, qkv_inputs
@@ -156,3 +156,45 @@ def test_prefill_calls_replay_in_graph():
         for i, (a, b) in enumerate(zip(outs, eager)):
             assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (rep, i)
         _ = (xq.float() @ wq[:64].float().t()).sum().item()   # eager work between replays
+
+
+@pytest.mark.gpu
+def test_int8_verify_calls_replay_in_graph():
+    """Verify-sized int8 calls on Qwen3-4B shapes (4 and 12 rows: x staged
+    once per workgroup in LDS, 8 and 16 staged rows) and the decode-sized
+    ones (1 row: the row kernels) captured in one HIP graph replay
+    bit-identically to the eager calls, several times, with eager work
+    between the replays."""
+    from llms_amd import kernels as K
+    from tests._util import ffn_inputs, qkv_inputs
+
+    _, wq = qkv_inputs(41, 1, 2560, 4096, 1024)
+    _, wg, wu = ffn_inputs(42, 1, 2560, 9728)
+    qq, sq = K.quantize_w8_per_row(wq.to(DEV))
+    qg, sg = K.quantize_w8_per_row(wg.to(DEV))
+    qu, su = K.quantize_w8_per_row(wu.to(DEV))
+    xs = [qkv_inputs(43 + M, M, 2560, 0, 0)[0].to(DEV) for M in (1, 4, 12)]
+
+    def calls():
+        out = []
+        for x in xs:
+            out += list(K.fused_qkv_w8(x, qq, sq, n_q=4096, n_k=1024))
+            out.append(K.fused_gate_up_silu_w8(x, qg, sg, qu, su))
+        return out
+
+    eager = [t.clone() for t in calls()]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls()                      # warm the allocator outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = calls()
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(outs, eager)):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (rep, i)
+        _ = (xs[2].float() @ wq[:64].to(DEV).float().t()).sum().item()   # eager work between replays
