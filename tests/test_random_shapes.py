@@ -145,3 +145,53 @@ def test_shapes_cover_the_regimes():
     assert any(65 <= m <= 256 for m in Ms) and any(m >= 512 for m in Ms)
     assert any(k % 64 == 0 for k in Ks) and any(k % 64 != 0 and k % 8 == 0 for k in Ks)
     assert any(k % 8 != 0 for k in Ks)
+
+
+def _verify8_shapes(n: int, seed: int = 77):
+    """(M, K, N, I): int8 shapes inside the x-staging verify kernel's domain
+    (2-16 rows, K a multiple of 64 from 2048 to 2560, at least 4096 outputs),
+    output widths with partial blocks of 16."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(2, 17)), 64 * int(rng.integers(32, 41)),
+             int(rng.integers(4096, 9001)), int(rng.integers(4096, 12001))) for _ in range(n)]
+
+
+VERIFY8_SHAPES = _verify8_shapes(8)
+
+
+@pytest.mark.parametrize("i", range(len(VERIFY8_SHAPES)))
+def test_random_int8_verify_shape(i):
+    """Seeded int8 shapes at spec-verify row counts with K from 2048 to 2560:
+    QKV-like, plain and gate-up calls against the oracle, every other case
+    with x as a row-strided view."""
+    M, K, N, inter = VERIFY8_SHAPES[i]
+    kern = _kernels()
+    tag = f"verify8 case {i}: M={M} K={K} N={N} I={inter}"
+    n_k = 512
+    x, w = qkv_inputs(7000 + i, M, K, N - 2 * n_k, n_k)
+    xd = _on_device(x, 3 * i + 1) if i % 2 else x.to(DEV)
+    qw, sw = _quant(w)
+    q, k, v = kern.fused_qkv_w8(xd, qw, sw, n_q=N - 2 * n_k, n_k=n_k)
+    y = torch.cat([q, k, v], -1).cpu()
+    out = ref.ref_qkv_w8_full(bits(x), qw.cpu().numpy(), sw.cpu().numpy(), N - 2 * n_k, n_k)
+    _check(y, out, f"{tag} int8 qkv")
+    y = kern.fused_linear_w8(xd, qw, sw).cpu()
+    _check(y, ref.ref_linear_w8(bits(x), qw.cpu().numpy(), sw.cpu().numpy()), f"{tag} int8 linear")
+
+    x, wg, wu = ffn_inputs(8000 + i, M, K, inter)
+    xd = _on_device(x, 3 * i + 1) if i % 2 else x.to(DEV)
+    qg, sg = _quant(wg)
+    qu, su = _quant(wu)
+    y = kern.fused_gate_up_silu_w8(xd, qg, sg, qu, su).cpu()
+    out = ref.ref_gate_up_silu_w8_full(bits(x), qg.cpu().numpy(), sg.cpu().numpy(),
+                                       qu.cpu().numpy(), su.cpu().numpy())
+    _check(y, out, f"{tag} int8 gate-up")
+
+
+def test_verify8_shapes_in_domain():
+    """The seeded draw stays inside the domain it claims, and reaches both
+    of the kernel's x stagings (up to 8 rows, and 9-16)."""
+    assert all(2 <= m <= 16 and 2048 <= k <= 2560 and k % 64 == 0 and n >= 4096 and i >= 4096
+               for m, k, n, i in VERIFY8_SHAPES)
+    assert any(m <= 8 for m, *_ in VERIFY8_SHAPES) and any(m > 8 for m, *_ in VERIFY8_SHAPES)
+    assert any(n % 16 for _, _, n, _ in VERIFY8_SHAPES)
