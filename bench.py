@@ -11,7 +11,9 @@ once in a HIP graph and replayed.
 Headline metric: HBM GB/s at M=1 on Qwen3-4B shapes =
 algorithmic bytes per layer pair (2K(N_qkv+2I) + 4MK + 2M(N_qkv+I)) x layers /
 step time. Also reported: TFLOP/s at M=2048 (prefill), the dominant kernel's
-roofline (per-launch HIP events on its stream), and the reference's unfused
+roofline (per-launch HIP events on its stream), the model's other BASELINE
+cells (``cells``: bf16 spec-verify at M=4 with hipBLASLt beside it, int8 at
+M=1, 4 and 2048; per-launch µs by graph replay), and the reference's unfused
 torch path timed on this host's CPU cores.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 100]
@@ -801,6 +803,11 @@ def config_line(torch, kern, shape, M: int, int8: bool, reps: int, hipblaslt: bo
     return out
 
 
+# BASELINE cells of the bench model reported beside the headline (M, int8):
+# spec-verify in bf16, and the int8 decode, verify and prefill configurations
+BENCH_CELLS = ((4, False), (1, True), (4, True), (2048, True))
+
+
 def configs_run(torch, kern, reps: int):
     """Both fused projections on every BASELINE configuration, one JSON line
     each (config_line)."""
@@ -862,6 +869,9 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cells", action="store_true",
+                    help="skip the other BASELINE cells of the model (verify and int8) that "
+                         "the default run reports beside the decode step")
     ap.add_argument("--counters", action="store_true",
                     help="run only the short fixed sequence used for rocprofv3 --pmc runs")
     ap.add_argument("--hipblaslt", action="store_true",
@@ -1044,6 +1054,16 @@ def main() -> int:
     del stack
     torch.cuda.empty_cache()
 
+    # other BASELINE cells of the same model, in the same run (config_line:
+    # graph replay over distinct weight sets; bf16 with hipBLASLt beside)
+    cells = None
+    if not args.no_cells:
+        cells = []
+        for M, int8 in BENCH_CELLS:
+            c = config_line(torch, kern, shape, M, int8, max(5, args.steps // 4))
+            cells.append(c)
+            log(f"cell M={M} {c['weights']}: qkv {c['qkv_us']} us, gate-up {c['gate_up_us']} us")
+
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -1090,6 +1110,7 @@ def main() -> int:
             "avg_launch_us": round(d_gu * 1e6, 3),
         },
         "prefill": prefill,
+        "cells": cells,
         "cpu_baseline": cpu,
         "device": dev_name,
     }
