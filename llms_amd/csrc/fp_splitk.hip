@@ -4,7 +4,11 @@
 // (QKV has N = 6144: 24 tiles of 256 rows).
 //
 // A workgroup owns a small output tile: BN weight rows (gate-up: BN/2 rows of
-// Wg and BN/2 of Wu, interleaved in 16-row groups) x BM rows of x. Its NW
+// Wg and BN/2 of Wu, interleaved in 16-row groups) x BM rows of x. A bf16
+// QKV tile may hold 24 rows: its second MFMA block then reads 8 rows past
+// the tile's (other bytes of the wave's own stage) into accumulator rows
+// that are never stored; the matrix core is idle enough in this regime for
+// that to cost nothing. Its NW
 // waves split K: wave w takes k-steps w, w + NW, w + 2 NW, ... (64 k each),
 // each wave with a private ring of NS LDS stages that it fills itself with
 // buffer_load_dwordx4 ... lds (8 tile rows x 128 B per instruction, whole
@@ -57,11 +61,13 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
   constexpr int WROW = kBK * WB;               // bytes of a weight tile row per step
   constexpr int WRPI = 1024 / WROW;            // weight rows per load instruction
   constexpr int WCPR = WROW / 16;              // 16-byte chunks per weight row
-  constexpr int FN = BN / 16, FM = BM / 16;    // MFMA sub-tiles (the whole tile per wave)
+  constexpr int FN = (BN + 15) / 16, FM = BM / 16;  // MFMA sub-tiles (the whole tile per wave)
   constexpr int IW = BN / WRPI, IX = BM / kRPI;  // load instructions per stage
   constexpr int kPerStep = IW + IX;
   constexpr int SW = BN * WROW, SX = BM * kBK * 2;  // bytes per wave and stage
-  static_assert(BN % 16 == 0 && BM % 16 == 0 && BN % WRPI == 0, "tile");
+  static_assert((BN % 16 == 0 || (BN % 8 == 0 && !GATEUP && !W8)) && BM % 16 == 0 &&
+                    BN % WRPI == 0,
+                "tile: whole 16-row blocks, or a last half block for bf16 QKV");
   static_assert(!GATEUP || BN % 32 == 0, "gate-up tiles hold whole gate/up 16-row pairs");
   static_assert(NS == 2 || NS == 3, "LDS stages");
   // the partial tiles of waves 1 .. NW-1 are summed in stage 0's space, FC
@@ -246,6 +252,7 @@ __global__ __launch_bounds__(NW * kWave) void splitk_kernel(StreamArgs a, int n_
 #pragma unroll
         for (int r = 0; r < 4; ++r) h[r] = gate_up_silu_bits(acc[i][j][r], acc[i + 1][j][r]);
       } else {
+        if (i * 16 + 4 * grp >= BN) continue;  // rows past a 24-row tile
         nb = c0 + i * 16 + 4 * grp;
 #pragma unroll
         for (int r = 0; r < 4; ++r) h[r] = f32_to_bf16_bits(acc[i][j][r]);
@@ -345,6 +352,15 @@ int launch_splitk(const StreamArgs& a, hipStream_t s) {
     if (a.M <= 64) return launch_splitk_cfg<32, 64, 4, 3, true, W8>(a, s);
     return launch_splitk_cfg<64, 64, 4, 2, true, W8>(a, s);
   } else {
+    // Qwen3-sized QKV (4096 < N <= 6144, K 2048..4096) at up to 16 rows:
+    // 24-row tiles with 8 waves, at most 256 of them, one per CU. The two
+    // libraries alternated on one box over 36 weight sets (µs): Qwen3-4B (K =
+    // 2560) at M = 3, 4, 8, 16 7.77, 7.83, 9.1, 9.55 -> 7.65, 7.65, 8.7, 9.25
+    // against 32-row tiles (192 of them; bit-identical, the same k order);
+    // Qwen3-8B (K = 4096) at M = 4, 16 11.17, 13.3 -> 10.95, 11.2 against
+    // 16-row tiles of 4 waves.
+    if (!W8 && a.M <= 16 && a.N > 4096 && a.N <= 6144 && a.K >= 2048 && a.K <= 4096)
+      return launch_splitk_cfg<24, 16, 8, 2, false, false>(a, s);
     // Qwen3-4B-sized QKV (4096 < N <= 8192, K 2048..3072) at up to 16 rows:
     // 32-row tiles with 8 waves (one box, µs at M = 3, 4, 8, 16: 8.11, 8.50,
     // 8.77, 9.85 -> 7.73, 8.02, 8.32, 8.80 against 16-row tiles of 4 waves;
