@@ -361,6 +361,12 @@ int launch_splitk(const StreamArgs& a, hipStream_t s) {
     // 16-row tiles of 4 waves.
     if (!W8 && a.M <= 16 && a.N > 4096 && a.N <= 6144 && a.K >= 2048 && a.K <= 4096)
       return launch_splitk_cfg<24, 16, 8, 2, false, false>(a, s);
+    // ... and at 17-64 rows: 8 waves of 32 x rows to 32 rows, then 4 waves of
+    // 64 with three LDS stages (same comparison, Qwen3-8B at M = 32, 48, 64:
+    // 15.1, 18.2, 19.0 -> 13.2, 17.1, 17.95 against 32-row tiles)
+    if (!W8 && a.M <= 64 && a.N > 4096 && a.N <= 6144 && a.K >= 2048 && a.K <= 4096)
+      return a.M <= 32 ? launch_splitk_cfg<24, 32, 8, 2, false, false>(a, s)
+                       : launch_splitk_cfg<24, 64, 4, 3, false, false>(a, s);
     // Qwen3-4B-sized QKV (4096 < N <= 8192, K 2048..3072) at up to 16 rows:
     // 32-row tiles with 8 waves (one box, µs at M = 3, 4, 8, 16: 8.11, 8.50,
     // 8.77, 9.85 -> 7.73, 8.02, 8.32, 8.80 against 16-row tiles of 4 waves;

@@ -578,13 +578,14 @@ def test_int8_gate_up_one_row_bit_exact(K):
 
 
 @pytest.mark.parametrize("M,K,N", [(3, 2560, 6144), (8, 2560, 6150), (16, 4096, 6144),
-                                   (5, 4096, 5000), (11, 2048, 6136)])
+                                   (5, 4096, 5000), (11, 2048, 6136), (24, 4096, 6144),
+                                   (33, 2560, 6150), (64, 4096, 5000), (50, 2048, 6144)])
 def test_qkv_verify_24_row_tiles(M, K, N):
-    """bf16 QKV at 3-16 rows with 4096 < N <= 6144 runs split-K tiles of 24
-    weight rows (at most 256 of them); their second MFMA block reaches 8 rows
-    past the tile, which must never be stored. Whole tiles (6144), a partial
-    last tile (6150, 5000, 6136) and K = 2048, 2560, 4096, against the
-    oracle."""
+    """bf16 QKV at 3-64 rows with 4096 < N <= 6144 runs split-K tiles of 24
+    weight rows (at most 256 of them; 16, 32 or 64 x rows); their second MFMA
+    block reaches 8 rows past the tile, which must never be stored. Whole
+    tiles (6144), a partial last tile (6150, 5000, 6136), partial x tiles
+    (33, 50) and K = 2048, 2560, 4096, against the oracle."""
     n_k = 512
     x, w = qkv_inputs(1500 + M, M, K, N - 2 * n_k, n_k)
     q, k, v = _kernels().triton_fused_qkv(x.to(DEV), w.to(DEV), n_q=N - 2 * n_k, n_k=n_k)
