@@ -345,6 +345,13 @@ int launch_splitk(const StreamArgs& a, hipStream_t s) {
     // on Qwen3-8B, K = 4096, they measured slower: 32.7 -> 39.1)
     if (a.M <= 16 && a.N >= 7680 && a.K <= 3072)
       return launch_splitk_cfg<96, 16, 4, 2, true, W8>(a, s);
+    // ... and at 17-64 rows (203 tiles on Qwen3-4B where 32-row tiles made
+    // 608; the two libraries alternated on one box, µs, M = 17, 24, 32, 40,
+    // 47: 26.9, 28.2, 30.2, 36.4, 37.3 -> 23.1, 23.6, 24.1, 27.8, 28.2; from
+    // 48 rows the staged tiles of fp_gemm.hip take these calls)
+    if (a.M <= 64 && a.N >= 7680 && a.K <= 3072)
+      return a.M <= 32 ? launch_splitk_cfg<96, 32, 4, 2, true, W8>(a, s)
+                       : launch_splitk_cfg<96, 64, 4, 2, true, W8>(a, s);
     if (a.M <= 16)
       return a.N <= 3072 && a.K >= 2560 ? launch_splitk_cfg<32, 16, 8, 2, true, W8>(a, s)
                          : launch_splitk_cfg<32, 16, 4, 3, true, W8>(a, s);

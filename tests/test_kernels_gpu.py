@@ -161,10 +161,11 @@ def test_qwen3_4b_gate_up_decode(M):
     check_ffn(M, M, K, I)
 
 
-@pytest.mark.parametrize("M", [8, 16])
+@pytest.mark.parametrize("M", [8, 16, 17, 32, 33, 47])
 def test_gate_up_verify_tiles_ragged(M):
-    """The 96-row split-K tiles of wide short-K gate-up at 8-16 rows with a
-    partial last tile (9700 outputs: 48 per tile), against the oracle."""
+    """The 96-row split-K tiles of wide short-K gate-up at 8-47 rows (16, 32
+    and 64 x rows) with a partial last tile (9700 outputs: 48 per tile) and
+    partial x tiles, against the oracle."""
     check_ffn(90 + M, M, 2560, 9700, label=f"gate-up verify tiles M={M} N=9700")
 
 
