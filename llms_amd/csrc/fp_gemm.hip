@@ -1517,6 +1517,7 @@ int64_t gemm_split_ws_floats(const GemmSplit& p, int64_t M, int64_t N, int64_t K
 
 GemmSplit gemm_split_plan_bf16(int64_t M, int64_t N, int64_t K, bool gateup) {
   if (small_round_tile(M, N, K, gateup) >= 0) return GemmSplit{-1, 1};
+  if (!gateup && splitk24_shape(M, N, K)) return GemmSplit{-1, 1};  // 24-row split-K tiles
   const GemmSplit p = gemm_split_plan(M, N, K, gateup);
   if (p.tile < 0 || K % (2 * kBK) != 0) return p;
   // The staged 96 x 64 four-wave tiles (three LDS stages), k split into

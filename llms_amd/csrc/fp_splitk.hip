@@ -366,12 +366,12 @@ int launch_splitk(const StreamArgs& a, hipStream_t s) {
     // against 32-row tiles (192 of them; bit-identical, the same k order);
     // Qwen3-8B (K = 4096) at M = 4, 16 11.17, 13.3 -> 10.95, 11.2 against
     // 16-row tiles of 4 waves.
-    if (!W8 && a.M <= 16 && a.N > 4096 && a.N <= 6144 && a.K >= 2048 && a.K <= 4096)
+    if (!W8 && a.M <= 16 && splitk24_shape(a.M, a.N, a.K))
       return launch_splitk_cfg<24, 16, 8, 2, false, false>(a, s);
     // ... and at 17-64 rows: 8 waves of 32 x rows to 32 rows, then 4 waves of
     // 64 with three LDS stages (same comparison, Qwen3-8B at M = 32, 48, 64:
     // 15.1, 18.2, 19.0 -> 13.2, 17.1, 17.95 against 32-row tiles)
-    if (!W8 && a.M <= 64 && a.N > 4096 && a.N <= 6144 && a.K >= 2048 && a.K <= 4096)
+    if (!W8 && splitk24_shape(a.M, a.N, a.K))
       return a.M <= 32 ? launch_splitk_cfg<24, 32, 8, 2, false, false>(a, s)
                        : launch_splitk_cfg<24, 64, 4, 3, false, false>(a, s);
     // Qwen3-4B-sized QKV (4096 < N <= 8192, K 2048..3072) at up to 16 rows:
